@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""bench.py — throughput of the MI355X dense-contraction hot path.
+
+One JSON line on stdout. The headline workload (`--workload dit`, default)
+is BASELINE configs[4]: the DiT/QwenImage transformer GEMMs in bf16 with f32
+accumulation at M=4096 (QKV 3072→9216, MLP-up 3072→12288 + GELU, MLP-down
+12288→3072). A "step" is one pass of the three Gemm calls (f32 activations
+in HBM, rounded to bf16 on their way in, bf16 weights packed once). `value`
+is step FLOPs / step wall time (TFLOPS).
+
+The other BASELINE configs are measured in the same run and reported under
+"workloads" (skip with --no-extra): BERT-base f32 projections,
+int8 MatMulInteger + DequantizeLinear and decode GEMV M=1/4/16
+(configs[3], weights rotated over 3 copies so HBM, not the 256 MB Infinity
+Cache, serves them).
+
+roofline: the dominant kernel's algorithmic FLOPs (or bytes) per launch over
+its average launch duration, timed with HIP events on the session stream
+(the stream the kernels run on). cpu_baseline: the reference's amd64 CPU
+algorithm restated in C++ (oracle/baseline.cpp, kind "port"), timed on a
+bounded row sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GEMM TFLOPS (bf16/fp32), int8 TOPS, GEMV HBM GB/s; % of MI355X roofline"
+PEAK = {"bf16": 2516.6, "f32": 157.3, "i8": 5033.2, "hbm": 8000.0}  # TFLOP/s, TOP/s, GB/s
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def normal32(rng, shape, scale):
+    return rng.normal(0, scale, shape).astype(np.float32)
+
+
+def time_steps(sess, step, steps: int, warmup: int):
+    for _ in range(warmup):
+        step()
+    sess.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    sess.sync()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def event_ms(sess, fn, reps: int) -> float:
+    """Average GPU time of fn() (HIP events on the session stream)."""
+    fn()
+    sess.sync()
+    sess.timer_start()
+    for _ in range(reps):
+        fn()
+    return sess.timer_stop() / reps
+
+
+# ---------------- workloads ----------------
+
+class Dit:
+    name = "dit"
+    shapes = [(3072, 9216, "qkv"), (3072, 12288, "mlp_up_gelu"), (12288, 3072, "mlp_down")]
+
+    def __init__(self, sess, L):
+        self.sess, self.L = sess, L
+        rng = np.random.default_rng(20260405)
+        self.M = 4096
+        self.a = {k: sess.to_device(rng.normal(0, 1, (self.M, k)).astype(np.float32)) for k in (3072, 12288)}
+        self.w, self.y, self.acts = [], [], []
+        for k, n, tag in self.shapes:
+            # f32 N(0, 0.02) weights, packed once as bf16 (RNE) by the library
+            self.w.append(sess.upload_weight(normal32(rng, (n, k), 0.02), trans=True, pack_dtype=L.DT_BF16))
+            self.y.append(sess.empty(L.DT_F32, (self.M, n)))
+            self.acts.append(L.ACT_GELU_ERF if tag.endswith("gelu") else L.ACT_NONE)
+        self.flops = sum(2.0 * self.M * n * k for k, n, _ in self.shapes)
+
+    def step(self):
+        for (k, n, _), w, y, act in zip(self.shapes, self.w, self.y, self.acts):
+            self.sess.gemm(self.a[k], w, y, self.M, act=act)
+
+    def kernel_roofline(self):
+        """The bf16 MFMA GEMM kernel alone: activations already bf16 (one launch per Gemm)."""
+        L, s = self.L, self.sess
+        a16 = {}
+        for k, t in self.a.items():
+            a16[k] = s.empty(L.DT_BF16, (self.M, k))
+            s.cast_bf16(t, a16[k])
+
+        def launches():
+            for (k, n, _), w, y, act in zip(self.shapes, self.w, self.y, self.acts):
+                s.gemm(a16[k], w, y, self.M, act=act, a_dtype=L.DT_BF16)
+
+        ms = event_ms(s, launches, 10) / len(self.shapes)
+        flops = self.flops / len(self.shapes)
+        for t in a16.values():
+            t.free()
+        achieved = flops / (ms * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK["bf16"], 4), "traffic": None,
+                "kernel": "gemm_kernel<bf16,256,192>", "avg_launch_us": round(ms * 1e3, 2),
+                "flops_per_launch": flops}
+
+    def cpu_baseline(self, threads: int, seconds: float):
+        import oracle
+
+        rng = np.random.default_rng(20260405)
+        rows = 144  # one MC block of the reference's blocking, per GEMM
+        packs = [oracle.PackedB(oracle.f32_to_bf16(normal32(rng, (n, k), 0.02)), trans_b=True, bf16=True)
+                 for k, n, _ in self.shapes]
+        a = {k: rng.normal(0, 1, (rows, k)).astype(np.float32) for k in (3072, 12288)}
+        outs = [np.empty((rows, n), np.float32) for _, n, _ in self.shapes]
+
+        def once():
+            for (k, n, tag), pb, o in zip(self.shapes, packs, outs):
+                oracle.base_sgemm(a[k], pb, gelu=tag.endswith("gelu"), threads=threads, out=o)
+
+        once()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            once()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or reps >= 10000:
+                break
+        flops = sum(2.0 * rows * n * k for k, n, _ in self.shapes)
+        return {"value": round(flops * reps / el / 1e12, 4), "unit": "TFLOPS", "cores": threads, "kind": "port",
+                "sample": f"the 3 DiT GEMMs on {rows} of 4096 rows (bf16 weights widened per panel, f32 A), "
+                          f"{reps} reps in {el:.1f} s"}
+
+
+class Bert:
+    name = "bert"
+    shapes = [(768, 2304, 0), (768, 768, 0), (768, 3072, 1), (3072, 768, 0)]
+
+    def __init__(self, sess, L):
+        self.sess, self.L = sess, L
+        rng = np.random.default_rng(1)
+        self.M = 1024
+        self.a = {k: sess.to_device(rng.normal(0, 1, (self.M, k)).astype(np.float32)) for k in (768, 3072)}
+        self.w, self.b, self.y = [], [], []
+        for k, n, _ in self.shapes:
+            self.w.append(sess.upload_weight(rng.normal(0, 0.02, (k, n)).astype(np.float32), trans=False,
+                                             pack_dtype=L.DT_F32))
+            self.b.append(sess.to_device(rng.normal(0, 0.02, n).astype(np.float32)))
+            self.y.append(sess.empty(L.DT_F32, (self.M, n)))
+        self.flops = sum(2.0 * self.M * n * k for k, n, _ in self.shapes)
+
+    def step(self):
+        L = self.L
+        for (k, n, gelu), w, b, y in zip(self.shapes, self.w, self.b, self.y):
+            self.sess.gemm(self.a[k], w, y, self.M, beta=1.0, c=b, c_mode=L.C_ROW,
+                           act=L.ACT_GELU_ERF if gelu else L.ACT_NONE)
+
+    def report(self, ms):
+        v = self.flops / (ms * 1e-3) / 1e12
+        return {"value": round(v, 2), "unit": "TFLOPS", "ms_per_step": round(ms, 4), "dtype": "f32",
+                "roofline_frac": round(v / PEAK["f32"], 4), "peak": PEAK["f32"]}
+
+
+class Int8:
+    name = "int8"
+
+    def __init__(self, sess, L):
+        self.sess, self.L = sess, L
+        rng = np.random.default_rng(3)
+        self.M, self.K, self.N = 1024, 768, 3072
+        self.a = sess.to_device(rng.integers(0, 256, (self.M, self.K)).astype(np.uint8), L.DT_U8)
+        self.w = sess.upload_weight(rng.integers(-127, 128, (self.K, self.N)).astype(np.int8), trans=False,
+                                    pack_dtype=L.DT_I8)
+        sc = (rng.uniform(0.001, 0.01, self.N).astype(np.float32) * np.float32(0.02)).astype(np.float32)
+        self.scale = sess.to_device(sc)
+        self.y = sess.empty(L.DT_F32, (self.M, self.N))
+        self.ops = 2.0 * self.M * self.N * self.K
+        self.bytes = self.M * self.K + self.K * self.N + 4 * self.M * self.N
+
+    def step(self):
+        self.sess.matmul_integer(self.a, self.w, self.M, 128, scale=self.scale, y_f32=self.y)
+
+    def report(self, ms):
+        tops = self.ops / (ms * 1e-3) / 1e12
+        gbs = self.bytes / (ms * 1e-3) / 1e9
+        return {"value": round(tops, 2), "unit": "TOPS", "ms_per_step": round(ms, 4), "dtype": "i8",
+                "GB_per_s": round(gbs, 1), "hbm_frac": round(gbs / PEAK["hbm"], 4),
+                "mfma_frac": round(tops / PEAK["i8"], 4)}
+
+
+class Decode:
+    name = "decode"
+    shapes = [(2048, 6144), (2048, 2048), (2048, 11264), (5632, 2048)]
+    copies = 3  # > 256 MB of weights in rotation: HBM, not the Infinity Cache
+
+    def __init__(self, sess, L, M=1):
+        self.sess, self.L, self.M = sess, L, M
+        rng = np.random.default_rng(4)
+        self.x = {k: sess.to_device(rng.normal(0, 1, (16, k)).astype(np.float32)) for k in (2048, 5632)}
+        self.w = [[sess.upload_weight(normal32(rng, (n, k), 0.02), trans=True, pack_dtype=L.DT_BF16)
+                   for k, n in self.shapes] for _ in range(self.copies)]
+        self.y = [sess.empty(L.DT_F32, (16, n)) for _, n in self.shapes]
+        self.i = 0
+        self.wbytes = sum(2.0 * n * k for k, n in self.shapes)
+
+    def bytes_step(self, M):
+        return self.wbytes + sum(4.0 * M * (k + n) for k, n in self.shapes)
+
+    def step(self, M=None):
+        M = M or self.M
+        ws = self.w[self.i % self.copies]
+        self.i += 1
+        for (k, n), w, y in zip(self.shapes, ws, self.y):
+            self.sess.gemm(self.x[k], w, y, M)
+
+    def report(self):
+        out = {}
+        for M in (1, 4, 16):
+            ms = time_steps(self.sess, lambda: self.step(M), 60, 10)
+            gbs = self.bytes_step(M) / (ms * 1e-3) / 1e9
+            out[f"m{M}"] = {"GB_per_s": round(gbs, 1), "us_per_step": round(ms * 1e3, 2),
+                            "hbm_frac": round(gbs / PEAK["hbm"], 4)}
+        # per-shape kernel time at M=1 (events over rotated launches)
+        per = {}
+        for j, (k, n) in enumerate(self.shapes):
+            def launches(j=j, k=k):
+                for c in range(self.copies):
+                    self.sess.gemm(self.x[k], self.w[c][j], self.y[j], 1)
+            ms = event_ms(self.sess, launches, 20) / self.copies
+            b = 2.0 * n * k + 4.0 * (k + n)
+            per[f"{k}x{n}"] = {"us": round(ms * 1e3, 2), "GB_per_s": round(b / (ms * 1e-3) / 1e9, 1)}
+        out["m1_per_shape"] = per
+        return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="dit", choices=["dit", "bert", "int8", "decode"])
+    ap.add_argument("--no-extra", action="store_true", help="measure only the headline workload")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        log("bench.py: this build measures one GPU (the path has no multi-GPU component); run with --gpus 1")
+        return 2
+
+    from ingot_amd import Session
+    from ingot_amd import _lib as L
+
+    sess = Session(0)
+    res = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
+    if args.workload == "dit":
+        log("dit: set-up")
+        wl = Dit(sess, L)
+        ms = time_steps(sess, wl.step, args.steps, args.warmup)
+        res.update({"value": round(wl.flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOPS", "ms_per_step": round(ms, 4),
+                    "dtype": "bf16",
+                    "config": {"workload": "DiT/QwenImage transformer GEMMs (BASELINE configs[4])", "M": 4096,
+                               "gemms": ["3072x9216", "3072x12288+gelu", "12288x3072"],
+                               "activations": "f32, bf16 RNE on load", "weights": "bf16", "accumulate": "f32",
+                               "global_batch": 4096, "parallelism": "none (1 GPU)"}})
+        log(f"dit: {res['value']} TFLOPS, {ms:.3f} ms/step; kernel roofline")
+        res["roofline"] = wl.kernel_roofline()
+        if not args.no_cpu_baseline:
+            threads = min(16, len(os.sched_getaffinity(0)))
+            log(f"dit: cpu baseline on {threads} threads")
+            res["cpu_baseline"] = wl.cpu_baseline(threads, args.cpu_seconds)
+    else:
+        wl = {"bert": Bert, "int8": Int8, "decode": Decode}[args.workload](sess, L)
+        if args.workload == "decode":
+            rep = wl.report()
+            res.update({"value": rep["m1"]["GB_per_s"], "unit": "GB/s", "ms_per_step": rep["m1"]["us_per_step"] / 1e3,
+                        "dtype": "bf16", "config": {"workload": "decode GEMV M=1 (BASELINE configs[3])"},
+                        "detail": rep})
+        else:
+            ms = time_steps(sess, wl.step, args.steps, args.warmup)
+            rep = wl.report(ms)
+            res.update({"value": rep["value"], "unit": rep["unit"], "ms_per_step": rep["ms_per_step"],
+                        "dtype": rep["dtype"], "config": {"workload": args.workload}, "detail": rep})
+    if args.workload == "dit" and not args.no_extra:
+        extra = {}
+        for cls in (Bert, Int8):
+            log(f"{cls.name}: measuring")
+            w = cls(sess, L)
+            extra[cls.name] = w.report(time_steps(sess, w.step, 50, 10))
+        log("decode: measuring")
+        extra["decode"] = Decode(sess, L).report()
+        res["workloads"] = extra
+    sess.close()
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,105 @@
+// Shared device/host definitions for the gfx950 kernels of libingot_rocm.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ingot_rocm.h"
+
+namespace ingot {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// float32 → bfloat16 bits, round to nearest even, NaN kept quiet.
+// Restates F32ToBF16 (kernels/gemm/bgemm.go:20-26) bit for bit.
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t b;
+    __builtin_memcpy(&b, &f, 4);
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((b >> 16) | 0x40u);
+    return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+
+__host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    uint32_t b = (uint32_t)h << 16;
+    float f;
+    __builtin_memcpy(&f, &b, 4);
+    return f;
+}
+
+// Float epilogue: y = post_scale·act(alpha·acc + beta·C) + post_shift.
+// The C operand follows the Gemm broadcast rules of ops/matmul.go:50-76.
+struct Epi {
+    float alpha, beta;
+    const float* c;
+    int64_t ldc;
+    int c_mode;
+    int act;
+    float act_alpha, act_beta;
+    int post;
+    float post_scale, post_shift;
+};
+
+// exp with the argument clamp of expScalar (kernels/vek/scalar.go:7-13).
+__device__ __forceinline__ float exp_clamped(float x) {
+    return __expf(fminf(fmaxf(x, -87.33654f), 88.37626f));
+}
+
+__device__ __forceinline__ float clamp01(float x) { return fminf(fmaxf(x, 0.f), 1.f); }
+
+// Activation set of ops/epilogue.go:48-73 plus the GELU forms of
+// ops/elementwise.go:411-414 (tanh) and kernels/vek/vek_generic.go:165-170 (erf).
+__device__ __forceinline__ float apply_act(float x, int act, float a, float b) {
+    switch (act) {
+        case INGOT_ACT_RELU: return fmaxf(x, 0.f);
+        case INGOT_ACT_GELU_ERF: return 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
+        case INGOT_ACT_GELU_TANH: {
+            float u = x + 0.044715f * x * x * x;
+            return 0.5f * x * (1.f + tanhf(0.7978845608028654f * u));
+        }
+        case INGOT_ACT_SIGMOID: return 1.f / (1.f + exp_clamped(-x));
+        case INGOT_ACT_SILU: return x / (1.f + exp_clamped(-x));
+        case INGOT_ACT_HARDSWISH: return x * clamp01(x / 6.f + 0.5f);
+        case INGOT_ACT_HARDSIGMOID: return clamp01(a * x + b);
+        case INGOT_ACT_CLIP: return fminf(fmaxf(x, a), b);
+        case INGOT_ACT_LEAKYRELU: return x < 0.f ? x * a : x;
+        default: return x;
+    }
+}
+
+__device__ __forceinline__ float epi_apply(const Epi& e, float acc, int64_t m, int64_t n) {
+    float v = e.alpha * acc;
+    switch (e.c_mode) {
+        case INGOT_C_FULL: v += e.beta * e.c[m * e.ldc + n]; break;
+        case INGOT_C_ROW: v += e.beta * e.c[n]; break;
+        case INGOT_C_COL: v += e.beta * e.c[m]; break;
+        case INGOT_C_SCALAR: v += e.beta * e.c[0]; break;
+        default: break;
+    }
+    if (e.act != INGOT_ACT_NONE) v = apply_act(v, e.act, e.act_alpha, e.act_beta);
+    if (e.post) v = v * e.post_scale + e.post_shift;
+    return v;
+}
+
+// Integer epilogue of MatMulInteger + DequantizeLinear:
+//   yi = acc + corr[n]                      (corr[n] = −za′·colSum[n], int32 wrap)
+//   yf = float32(yi − dq_zp) · scale[n or 0]
+struct QEpi {
+    const int32_t* colsum;
+    int32_t neg_za;  // −za′ (za′ = za − 128 for u8 activations shifted to s8)
+    int32_t* yi;
+    float* yf;
+    const float* scale;
+    int64_t n_scale;
+    int32_t dq_zp;
+};
+
+__device__ __forceinline__ int32_t wrap_mul(int32_t a, int32_t b) {
+    return (int32_t)((uint32_t)a * (uint32_t)b);
+}
+__device__ __forceinline__ int32_t wrap_add(int32_t a, int32_t b) {
+    return (int32_t)((uint32_t)a + (uint32_t)b);
+}
+
+}  // namespace ingot

@@ -1,0 +1,229 @@
+// Memory-bound helper kernels: weight and activation packing, DequantizeLinear,
+// the standalone activation / bias pass, the f32 → bf16 cast and fills.
+
+#include "kernels.hpp"
+
+namespace ingot {
+
+namespace {
+
+__device__ __forceinline__ float load_f(const void* p, int dt, int64_t i) {
+    switch (dt) {
+        case INGOT_DT_F32: return ((const float*)p)[i];
+        case INGOT_DT_BF16: return bf16_to_f32(((const uint16_t*)p)[i]);
+        default: return 0.f;
+    }
+}
+
+__device__ __forceinline__ int32_t load_i(const void* p, int dt, int64_t i) {
+    switch (dt) {
+        case INGOT_DT_U8: return (int32_t)((const uint8_t*)p)[i];
+        case INGOT_DT_I8: return (int32_t)((const int8_t*)p)[i];
+        case INGOT_DT_I32: return ((const int32_t*)p)[i];
+        default: return 0;
+    }
+}
+
+inline unsigned grid_for(int64_t work, int per_block) {
+    int64_t b = (work + per_block - 1) / per_block;
+    if (b > (1 << 20)) b = 1 << 20;
+    if (b < 1) b = 1;
+    return (unsigned)b;
+}
+
+// dst[j][k] (np × kp, dst_kind) = src element (j, k) of the logical [n][k]
+// weight, zero outside n × k. One thread per destination element.
+__global__ void pack_weight_kernel(const void* src, int src_dt, int64_t ld, int trans, int64_t n, int64_t k,
+                                   void* dst, int dst_kind, int64_t np, int64_t kp) {
+    const int64_t total = np * kp;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t j = i / kp, kk = i - j * kp;
+        const bool in = j < n && kk < k;
+        const int64_t si = trans ? j * ld + kk : kk * ld + j;
+        if (dst_kind == KIND_I8) {
+            ((int8_t*)dst)[i] = in ? ((const int8_t*)src)[si] : (int8_t)0;
+        } else {
+            const float v = in ? load_f(src, src_dt, si) : 0.f;
+            if (dst_kind == KIND_BF16) {
+                ((uint16_t*)dst)[i] = (in && src_dt == INGOT_DT_BF16) ? ((const uint16_t*)src)[si] : f32_to_bf16(v);
+            } else {
+                ((float*)dst)[i] = v;
+            }
+        }
+    }
+}
+
+// One wave per row: colsum[j] = Σ_k packed[j][k] (int32 wrap-around).
+__global__ void colsum_kernel(const int8_t* packed, int64_t kp, int64_t n, int32_t* colsum) {
+    const int64_t j = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (j >= n) return;
+    uint32_t s = 0;
+    for (int64_t k = lane; k < kp; k += 64) s += (uint32_t)(int32_t)packed[j * kp + k];
+    for (int off = 32; off > 0; off >>= 1) s += (uint32_t)__shfl_xor((int)s, off);
+    if (lane == 0) colsum[j] = (int32_t)s;
+}
+
+// Packs activations into [m][kl] rows of dst_kind, zero padded beyond k.
+// Each thread produces one 16-byte chunk of a destination row.
+template <int KD>
+__global__ void pack_a_kernel(const void* src, int src_dt, int64_t lda, int trans, int64_t m, int64_t k,
+                              int64_t src_stride, void* dst, int64_t kl, int64_t dst_stride) {
+    constexpr int EPC = KD == KIND_BF16 ? 8 : (KD == KIND_F32 ? 4 : 16);  // elements per chunk
+    const int64_t chunks_per_row = kl / EPC;
+    const int64_t total = m * chunks_per_row;
+    const int b = blockIdx.y;
+    const char* sb = (const char*)src;
+    const int esz = src_dt == INGOT_DT_F32 ? 4 : (src_dt == INGOT_DT_BF16 ? 2 : 1);
+    sb += (int64_t)b * src_stride * esz;
+    for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < total; c += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = c / chunks_per_row;
+        const int64_t k0 = (c - row * chunks_per_row) * EPC;
+        i32x4_t out;
+        if (KD == KIND_I8) {
+            uint8_t v[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int64_t kk = k0 + e;
+                uint8_t x = 0;
+                if (kk < k) {
+                    const int64_t si = trans ? kk * lda + row : row * lda + kk;
+                    x = ((const uint8_t*)sb)[si];
+                    if (src_dt == INGOT_DT_U8) x ^= 0x80;
+                }
+                v[e] = x;
+            }
+            __builtin_memcpy(&out, v, 16);
+        } else if (KD == KIND_BF16) {
+            uint16_t v[8];
+            if (!trans && src_dt == INGOT_DT_F32 && k0 + 8 <= k && ((row * lda + k0) & 3) == 0 &&
+                (((uintptr_t)sb) & 15) == 0) {
+                const f32x4_t* s4 = (const f32x4_t*)((const float*)sb + row * lda + k0);
+                const f32x4_t lo = s4[0], hi = s4[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = f32_to_bf16(lo[e]);
+                    v[e + 4] = f32_to_bf16(hi[e]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int64_t kk = k0 + e;
+                    uint16_t x = 0;
+                    if (kk < k) {
+                        const int64_t si = trans ? kk * lda + row : row * lda + kk;
+                        x = src_dt == INGOT_DT_BF16 ? ((const uint16_t*)sb)[si] : f32_to_bf16(((const float*)sb)[si]);
+                    }
+                    v[e] = x;
+                }
+            }
+            __builtin_memcpy(&out, v, 16);
+        } else {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t kk = k0 + e;
+                v[e] = kk < k ? load_f(sb, src_dt, trans ? kk * lda + row : row * lda + kk) : 0.f;
+            }
+            __builtin_memcpy(&out, v, 16);
+        }
+        const int esz_d = KD == KIND_BF16 ? 2 : (KD == KIND_F32 ? 4 : 1);
+        char* db = (char*)dst + ((int64_t)b * dst_stride + row * kl + k0) * esz_d;
+        *(i32x4_t*)db = out;
+    }
+}
+
+__global__ void dequant_kernel(const void* x, int x_dt, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
+                               const void* zp, int zp_dt, int64_t n_zp, float* y) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t c = n_scale == 1 ? 0 : (i / inner) % n_scale;
+        int32_t z = 0;
+        if (zp) z = load_i(zp, zp_dt, n_zp > 1 ? c : 0);
+        y[i] = (float)wrap_add(load_i(x, x_dt, i), -z) * scale[c];
+    }
+}
+
+__global__ void activation_kernel(const float* x, float* y, int64_t rows, int64_t cols, const float* bias, int act,
+                                  float a, float b, int post, float ps, float pb) {
+    const int64_t total = rows * cols;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        float v = x[i];
+        if (bias) v += bias[i % cols];
+        if (act != INGOT_ACT_NONE) v = apply_act(v, act, a, b);
+        if (post) v = v * ps + pb;
+        y[i] = v;
+    }
+}
+
+__global__ void cast_bf16_kernel(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = f32_to_bf16(x[i]);
+}
+
+__global__ void fill_kernel(uint8_t* d, uint8_t v, size_t bytes) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < bytes; i += (size_t)gridDim.x * blockDim.x)
+        d[i] = v;
+}
+
+}  // namespace
+
+hipError_t launch_pack_weight(const void* src, int src_dtype, int64_t ld, int trans, int64_t n, int64_t k, void* dst,
+                              GemmKind dst_kind, int64_t np, int64_t kp, hipStream_t st) {
+    hipLaunchKernelGGL(pack_weight_kernel, dim3(grid_for(np * kp, 256)), dim3(256), 0, st, src, src_dtype, ld, trans, n,
+                       k, dst, (int)dst_kind, np, kp);
+    return hipGetLastError();
+}
+
+hipError_t launch_colsum_i8(const int8_t* packed, int64_t kp, int64_t n, int32_t* colsum, hipStream_t st) {
+    hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, packed, kp, n, colsum);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_a(const void* src, int src_dtype, int64_t lda, int trans, int64_t m, int64_t k,
+                         int64_t src_stride, void* dst, GemmKind dst_kind, int64_t kl, int64_t dst_stride, int batch,
+                         hipStream_t st) {
+    const int epc = dst_kind == KIND_BF16 ? 8 : (dst_kind == KIND_F32 ? 4 : 16);
+    dim3 grid(grid_for(m * (kl / epc), 256), batch);
+    switch (dst_kind) {
+        case KIND_BF16:
+            hipLaunchKernelGGL(pack_a_kernel<KIND_BF16>, grid, dim3(256), 0, st, src, src_dtype, lda, trans, m, k,
+                               src_stride, dst, kl, dst_stride);
+            break;
+        case KIND_F32:
+            hipLaunchKernelGGL(pack_a_kernel<KIND_F32>, grid, dim3(256), 0, st, src, src_dtype, lda, trans, m, k,
+                               src_stride, dst, kl, dst_stride);
+            break;
+        case KIND_I8:
+            hipLaunchKernelGGL(pack_a_kernel<KIND_I8>, grid, dim3(256), 0, st, src, src_dtype, lda, trans, m, k,
+                               src_stride, dst, kl, dst_stride);
+            break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant(const void* x, int x_dtype, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
+                          const void* zp, int zp_dtype, int64_t n_zp, float* y, hipStream_t st) {
+    hipLaunchKernelGGL(dequant_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, x, x_dtype, n, scale, n_scale,
+                       inner < 1 ? 1 : inner, zp, zp_dtype, n_zp, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_activation(const float* x, float* y, int64_t rows, int64_t cols, const float* bias, int act, float a,
+                             float b, int post, float ps, float pb, hipStream_t st) {
+    hipLaunchKernelGGL(activation_kernel, dim3(grid_for(rows * cols, 256)), dim3(256), 0, st, x, y, rows, cols, bias,
+                       act, a, b, post, ps, pb);
+    return hipGetLastError();
+}
+
+hipError_t launch_cast_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t st) {
+    hipLaunchKernelGGL(cast_bf16_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t st) {
+    hipLaunchKernelGGL(fill_kernel, dim3(grid_for((int64_t)bytes, 256)), dim3(256), 0, st, (uint8_t*)dst,
+                       (uint8_t)value, bytes);
+    return hipGetLastError();
+}
+
+}  // namespace ingot

@@ -1,0 +1,79 @@
+// Internal launch interface between the runtime (runtime.cpp) and the gfx950
+// kernels (gemm_mfma.hip, gemv_bf16.hip, elementwise.hip).
+#pragma once
+
+#include "common.hpp"
+
+namespace ingot {
+
+// Element kind of a packed GEMM operand pair (A and B share it).
+enum GemmKind { KIND_BF16 = 0, KIND_F32 = 1, KIND_I8 = 2 };
+
+// Every kernel row of A and B is read in 128-byte k-tiles: 64 bf16, 32 f32 or
+// 128 int8 elements. Packed operands are zero padded to whole k-tiles.
+constexpr int KTILE_BYTES = 128;
+
+struct GemmArgs {
+    const char* a;       // A rows [M][...] (row pitch lda_bytes), k-contiguous
+    int64_t lda_bytes;
+    const char* b;       // packed weight [b_rows][...] (row pitch ldb_bytes)
+    int64_t ldb_bytes;
+    int M, N;
+    int kt;              // number of 128-byte k-tiles to reduce over
+    int b_rows;          // allocated rows of b (loads clamp to it)
+    int tiles_m, tiles_n;
+    int64_t stride_a_bytes;  // per blockIdx.y batch item
+    int64_t stride_y;        // elements, per batch item
+    int a_xor;               // int8: flip the sign bit of A bytes (u8 → s8)
+    void* y;
+    int64_t ldy;
+    Epi epi;
+    QEpi qepi;
+};
+
+struct GemmConfig {
+    int bm, bn;
+    int occupancy;   // workgroups per CU the tile allows
+    float eff;       // relative per-CU efficiency (tile-size heuristic)
+};
+
+// Tile configurations compiled for `kind`; index used by launch_gemm.
+int gemm_configs(GemmKind kind, const GemmConfig** out);
+hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hipStream_t st);
+
+struct GemvArgs {
+    const float* x;
+    int64_t ldx;
+    int M, K;
+    const uint16_t* w;   // packed bf16 [>= 64·ceil(N/64)][ldw]
+    int64_t ldw;
+    int N;
+    int S;               // k splits
+    int KS;              // k per split (multiple of 256)
+    float* part;         // S > 1: partial sums [ceil(N/64)][S][M][64]
+    unsigned* cnt;       // S > 1: zeroed arrival counters, one per 64-row block
+    Epi epi;
+    float* y;
+    int64_t ldy;
+};
+hipError_t launch_gemv_bf16(const GemvArgs& a, hipStream_t st);
+
+// Packs a weight into [np][kp] of dst_kind, zero padded. src_dtype is an
+// INGOT_DT_* code; trans = 1: src is [n][k] (row pitch ld), 0: src is [k][n].
+hipError_t launch_pack_weight(const void* src, int src_dtype, int64_t ld, int trans, int64_t n, int64_t k,
+                              void* dst, GemmKind dst_kind, int64_t np, int64_t kp, hipStream_t st);
+// colsum[j] = Σ_k packed[j][k] over an int8 packed weight.
+hipError_t launch_colsum_i8(const int8_t* packed, int64_t kp, int64_t n, int32_t* colsum, hipStream_t st);
+// Packs activations A[M][K] (or [K][M] when trans) into [M][kl] of dst_kind
+// (kl = whole k-tiles), batch items at src_stride / dst_stride elements.
+hipError_t launch_pack_a(const void* src, int src_dtype, int64_t lda, int trans, int64_t m, int64_t k,
+                         int64_t src_stride, void* dst, GemmKind dst_kind, int64_t kl, int64_t dst_stride, int batch,
+                         hipStream_t st);
+hipError_t launch_dequant(const void* x, int x_dtype, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
+                          const void* zp, int zp_dtype, int64_t n_zp, float* y, hipStream_t st);
+hipError_t launch_activation(const float* x, float* y, int64_t rows, int64_t cols, const float* bias, int act,
+                             float a, float b, int post, float ps, float pb, hipStream_t st);
+hipError_t launch_cast_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t st);
+hipError_t launch_fill(void* dst, int value, size_t bytes, hipStream_t st);
+
+}  // namespace ingot

@@ -1,0 +1,642 @@
+// Host runtime of libingot_rocm: sessions, device pool, constant-weight packs
+// and the kernel-layer entry points of include/ingot_rocm.h.
+//
+// A session is the ROCm counterpart of the Metal GPUSession's device state
+// (graph/gpu_darwin_arm64.go:96-148): one HIP stream, a size-classed device
+// pool for op outputs (tensor.Pool, tensor/pool.go:10-60), a growable
+// workspace for packed activations and split-K partials, and the table of
+// packed constant weights (bCache / bf16Packs / bWeights:
+// ops/matmul.go:200-280, ops/quant.go:803-829).
+
+#include "runtime.hpp"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+using namespace ingot;
+
+namespace {
+
+thread_local std::string g_err;
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+int elem_size(int dt) {
+    switch (dt) {
+        case INGOT_DT_F32:
+        case INGOT_DT_I32: return 4;
+        case INGOT_DT_F16:
+        case INGOT_DT_BF16:
+        case INGOT_DT_I16: return 2;
+        case INGOT_DT_I8:
+        case INGOT_DT_U8:
+        case INGOT_DT_BOOL: return 1;
+        case INGOT_DT_I64: return 8;
+    }
+    return 0;
+}
+
+// elements of a kind per 128-byte k-tile
+int ktile_elems(GemmKind k) { return k == KIND_BF16 ? 64 : (k == KIND_F32 ? 32 : 128); }
+int kind_size(GemmKind k) { return k == KIND_BF16 ? 2 : (k == KIND_F32 ? 4 : 1); }
+
+// Picks the tile configuration with the least estimated time: full rounds of
+// num_cus·occupancy workgroups, each round as long as the most loaded CU.
+int pick_config(GemmKind kind, int64_t M, int64_t N, int64_t batch, int num_cus) {
+    const char* force = getenv("INGOT_GEMM_CFG");
+    const GemmConfig* c;
+    const int n = gemm_configs(kind, &c);
+    if (force && *force) {
+        const int f = atoi(force);
+        if (f >= 0 && f < n) return f;
+    }
+    int best = 0;
+    double best_t = 1e300;
+    for (int i = 0; i < n; ++i) {
+        const int64_t tiles = ((M + c[i].bm - 1) / c[i].bm) * ((N + c[i].bn - 1) / c[i].bn) * batch;
+        const int64_t slots = (int64_t)num_cus * c[i].occupancy;
+        const int64_t rounds = (tiles + slots - 1) / slots;
+        const int64_t per_cu = std::min<int64_t>(c[i].occupancy, (tiles + num_cus - 1) / num_cus);
+        const double t = (double)rounds * (double)per_cu * c[i].bm * c[i].bn / c[i].eff;
+        if (t < best_t * 0.999) {
+            best_t = t;
+            best = i;
+        }
+    }
+    return best;
+}
+
+bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
+
+}  // namespace
+
+namespace ingot {
+
+int fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(e == hipErrorOutOfMemory ? INGOT_ENOMEM : INGOT_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+int session_enter(ingot_rocm_session* s) {
+    if (!s) return fail(INGOT_EINVAL, "nil session");
+    hipError_t e = hipSetDevice(s->device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    return INGOT_OK;
+}
+
+int ws_reserve(ingot_rocm_session* s, size_t bytes, void** out) {
+    if (bytes > s->ws_bytes) {
+        hipError_t e = hipStreamSynchronize(s->stream);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        if (s->ws) (void)hipFree(s->ws);
+        s->ws = nullptr;
+        s->ws_bytes = 0;
+        const size_t nb = (size_t)round_up((int64_t)std::max(bytes, (size_t)1 << 21), (int64_t)1 << 21);
+        e = hipMalloc(&s->ws, nb);
+        if (e != hipSuccess) return hip_fail(e, "workspace hipMalloc");
+        s->ws_bytes = nb;
+    }
+    *out = s->ws;
+    return INGOT_OK;
+}
+
+void* pool_get(ingot_rocm_session* s, size_t bytes) {
+    size_t cls = 256;
+    while (cls < bytes) cls <<= 1;
+    auto it = s->free_bufs.find(cls);
+    if (it != s->free_bufs.end() && !it->second.empty()) {
+        void* p = it->second.back();
+        it->second.pop_back();
+        return p;
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, cls) != hipSuccess) return nullptr;
+    s->buf_class[p] = cls;
+    return p;
+}
+
+void pool_put(ingot_rocm_session* s, void* p) {
+    auto it = s->buf_class.find(p);
+    if (it == s->buf_class.end()) return;
+    s->free_bufs[it->second].push_back(p);
+}
+
+Epi make_epi(const ingot_rocm_gemm_args* a) {
+    Epi e;
+    e.alpha = a->alpha;
+    e.beta = a->beta;
+    e.c = a->d_c;
+    e.ldc = a->ldc;
+    e.c_mode = (a->d_c && a->beta != 0.f) ? a->c_mode : INGOT_C_NONE;
+    e.act = a->act;
+    e.act_alpha = a->act_alpha;
+    e.act_beta = a->act_beta;
+    e.post = a->post;
+    e.post_scale = a->post_scale;
+    e.post_shift = a->post_shift;
+    return e;
+}
+
+int check_epi(const ingot_rocm_gemm_args* a) {
+    if (a->act < INGOT_ACT_NONE || a->act > INGOT_ACT_LEAKYRELU) return fail(INGOT_EINVAL, "unknown activation %d", a->act);
+    if (a->d_c && a->beta != 0.f) {
+        if (a->c_mode < INGOT_C_NONE || a->c_mode > INGOT_C_SCALAR)
+            return fail(INGOT_EINVAL, "unknown C broadcast mode %d", a->c_mode);
+        if (a->c_mode == INGOT_C_FULL && a->ldc < a->N) return fail(INGOT_EINVAL, "ldc %lld < N %lld", (long long)a->ldc, (long long)a->N);
+    }
+    return INGOT_OK;
+}
+
+}  // namespace ingot
+
+// ======================= C ABI =======================
+
+extern "C" {
+
+const char* ingot_rocm_last_error(void) { return g_err.c_str(); }
+
+const char* ingot_rocm_version(void) { return "ingot-rocm 0.1 (gfx950)"; }
+
+int ingot_rocm_open(int device, ingot_rocm_session** out) {
+    if (!out) return fail(INGOT_EINVAL, "nil out");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= n) return fail(INGOT_EINVAL, "device %d out of range (%d devices)", device, n);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(INGOT_EDEVICE, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+    auto* s = new ingot_rocm_session();
+    s->device = device;
+    s->num_cus = prop.multiProcessorCount;
+    e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&s->t0);
+    if (e == hipSuccess) e = hipEventCreate(&s->t1);
+    if (e == hipSuccess) e = hipMalloc((void**)&s->counters, sizeof(unsigned) * ingot_rocm_session::kCounters);
+    if (e == hipSuccess) e = launch_fill(s->counters, 0, sizeof(unsigned) * ingot_rocm_session::kCounters, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) {
+        int rc = hip_fail(e, "session set-up");
+        ingot_rocm_close(s);
+        return rc;
+    }
+    *out = s;
+    return INGOT_OK;
+}
+
+int ingot_rocm_close(ingot_rocm_session* s) {
+    if (!s) return INGOT_OK;
+    (void)hipSetDevice(s->device);
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    for (auto* w : s->weights) {
+        if (w->data) (void)hipFree(w->data);
+        if (w->colsum) (void)hipFree(w->colsum);
+        delete w;
+    }
+    for (auto& kv : s->buf_class) (void)hipFree(kv.first);
+    if (s->ws) (void)hipFree(s->ws);
+    if (s->counters) (void)hipFree(s->counters);
+    if (s->t0) (void)hipEventDestroy(s->t0);
+    if (s->t1) (void)hipEventDestroy(s->t1);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+    return INGOT_OK;
+}
+
+int ingot_rocm_sync(ingot_rocm_session* s) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    hipError_t e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    return INGOT_OK;
+}
+
+int ingot_rocm_stream(ingot_rocm_session* s, void** stream) {
+    if (!s || !stream) return fail(INGOT_EINVAL, "nil argument");
+    *stream = (void*)s->stream;
+    return INGOT_OK;
+}
+
+int ingot_rocm_device_alloc(ingot_rocm_session* s, size_t bytes, void** d_out) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!d_out) return fail(INGOT_EINVAL, "nil out");
+    hipError_t e = hipMalloc(d_out, bytes ? bytes : 1);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+    return INGOT_OK;
+}
+
+int ingot_rocm_device_free(ingot_rocm_session* s, void* d_ptr) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!d_ptr) return INGOT_OK;
+    hipError_t e = hipStreamSynchronize(s->stream);
+    if (e == hipSuccess) e = hipFree(d_ptr);
+    if (e != hipSuccess) return hip_fail(e, "hipFree");
+    return INGOT_OK;
+}
+
+int ingot_rocm_host_alloc(ingot_rocm_session* s, size_t bytes, void** h_out) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!h_out) return fail(INGOT_EINVAL, "nil out");
+    hipError_t e = hipHostMalloc(h_out, bytes ? bytes : 1, hipHostMallocDefault);
+    if (e != hipSuccess) return hip_fail(e, "hipHostMalloc");
+    return INGOT_OK;
+}
+
+int ingot_rocm_host_free(ingot_rocm_session* s, void* h_ptr) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!h_ptr) return INGOT_OK;
+    hipError_t e = hipStreamSynchronize(s->stream);
+    if (e == hipSuccess) e = hipHostFree(h_ptr);
+    if (e != hipSuccess) return hip_fail(e, "hipHostFree");
+    return INGOT_OK;
+}
+
+static int copy_sync(ingot_rocm_session* s, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!bytes) return INGOT_OK;
+    if (!dst || !src) return fail(INGOT_EINVAL, "nil pointer");
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
+    return INGOT_OK;
+}
+
+int ingot_rocm_memcpy_h2d(ingot_rocm_session* s, void* d_dst, const void* h_src, size_t bytes) {
+    return copy_sync(s, d_dst, h_src, bytes, hipMemcpyHostToDevice);
+}
+int ingot_rocm_memcpy_d2h(ingot_rocm_session* s, void* h_dst, const void* d_src, size_t bytes) {
+    return copy_sync(s, h_dst, d_src, bytes, hipMemcpyDeviceToHost);
+}
+int ingot_rocm_memcpy_d2d(ingot_rocm_session* s, void* d_dst, const void* d_src, size_t bytes) {
+    return copy_sync(s, d_dst, d_src, bytes, hipMemcpyDeviceToDevice);
+}
+
+int ingot_rocm_memset(ingot_rocm_session* s, void* d_dst, int value, size_t bytes) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!bytes) return INGOT_OK;
+    if (!d_dst) return fail(INGOT_EINVAL, "nil pointer");
+    hipError_t e = launch_fill(d_dst, value, bytes, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "fill");
+    return INGOT_OK;
+}
+
+int ingot_rocm_timer_start(ingot_rocm_session* s) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    hipError_t e = hipEventRecord(s->t0, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+    return INGOT_OK;
+}
+
+int ingot_rocm_timer_stop(ingot_rocm_session* s, float* ms) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!ms) return fail(INGOT_EINVAL, "nil out");
+    hipError_t e = hipEventRecord(s->t1, s->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(s->t1);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, s->t0, s->t1);
+    if (e != hipSuccess) return hip_fail(e, "timer");
+    return INGOT_OK;
+}
+
+// ---------------- weights ----------------
+
+static int weight_pack(ingot_rocm_session* s, int src_dtype, int pack_dtype, int64_t rows, int64_t cols, int64_t ld,
+                       int trans, const void* src, bool host, ingot_rocm_weight** out) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!out) return fail(INGOT_EINVAL, "nil out");
+    *out = nullptr;
+    if (rows < 1 || cols < 1 || ld < cols || !src)
+        return fail(INGOT_EINVAL, "weight: need rows, cols >= 1, ld >= cols and data (rows=%lld cols=%lld ld=%lld)",
+                    (long long)rows, (long long)cols, (long long)ld);
+    GemmKind kind;
+    if (pack_dtype == INGOT_DT_F32 && src_dtype == INGOT_DT_F32) kind = KIND_F32;
+    else if (pack_dtype == INGOT_DT_BF16 && (src_dtype == INGOT_DT_F32 || src_dtype == INGOT_DT_BF16)) kind = KIND_BF16;
+    else if (pack_dtype == INGOT_DT_I8 && src_dtype == INGOT_DT_I8) kind = KIND_I8;
+    else return fail(INGOT_EINVAL, "weight: cannot pack dtype %d as %d", src_dtype, pack_dtype);
+    const int64_t n = trans ? rows : cols, k = trans ? cols : rows;
+    if (n > (int64_t)1 << 30 || k > (int64_t)1 << 30) return fail(INGOT_EINVAL, "weight too large");
+    auto* w = new ingot_rocm_weight();
+    w->pack_dtype = pack_dtype;
+    w->kind = kind;
+    w->n = n;
+    w->k = k;
+    w->np = round_up(n, 256);
+    w->kp = round_up(k, 256);
+    const int esz = elem_size(src_dtype);
+    const size_t src_bytes = (size_t)((rows - 1) * ld + cols) * esz;
+    const void* dsrc = src;
+    void* tmp = nullptr;
+    hipError_t e = hipMalloc(&w->data, (size_t)(w->np * w->kp) * kind_size(kind));
+    if (e == hipSuccess && kind == KIND_I8) e = hipMalloc((void**)&w->colsum, sizeof(int32_t) * w->np);
+    if (e == hipSuccess && host) {
+        e = hipMalloc(&tmp, src_bytes);
+        if (e == hipSuccess) e = hipMemcpyAsync(tmp, src, src_bytes, hipMemcpyHostToDevice, s->stream);
+        dsrc = tmp;
+    }
+    if (e == hipSuccess) e = launch_pack_weight(dsrc, src_dtype, ld, trans, n, k, w->data, kind, w->np, w->kp, s->stream);
+    if (e == hipSuccess && kind == KIND_I8) e = launch_colsum_i8((const int8_t*)w->data, w->kp, w->np, w->colsum, s->stream);
+    if (host && e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (tmp) (void)hipFree(tmp);
+    if (e != hipSuccess) {
+        if (w->data) (void)hipFree(w->data);
+        if (w->colsum) (void)hipFree(w->colsum);
+        delete w;
+        return hip_fail(e, "weight pack");
+    }
+    s->weights.push_back(w);
+    *out = w;
+    return INGOT_OK;
+}
+
+int ingot_rocm_weight_upload(ingot_rocm_session* s, int src_dtype, int pack_dtype, int64_t rows, int64_t cols,
+                             int64_t ld, int trans, const void* h_src, ingot_rocm_weight** out) {
+    return weight_pack(s, src_dtype, pack_dtype, rows, cols, ld, trans, h_src, true, out);
+}
+
+int ingot_rocm_weight_pack_device(ingot_rocm_session* s, int src_dtype, int pack_dtype, int64_t rows, int64_t cols,
+                                  int64_t ld, int trans, const void* d_src, ingot_rocm_weight** out) {
+    return weight_pack(s, src_dtype, pack_dtype, rows, cols, ld, trans, d_src, false, out);
+}
+
+int ingot_rocm_weight_free(ingot_rocm_session* s, ingot_rocm_weight* w) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!w) return INGOT_OK;
+    auto it = std::find(s->weights.begin(), s->weights.end(), w);
+    if (it == s->weights.end()) return fail(INGOT_EINVAL, "weight does not belong to this session");
+    s->weights.erase(it);
+    (void)hipStreamSynchronize(s->stream);
+    if (w->data) (void)hipFree(w->data);
+    if (w->colsum) (void)hipFree(w->colsum);
+    delete w;
+    return INGOT_OK;
+}
+
+int ingot_rocm_weight_info(const ingot_rocm_weight* w, int64_t* n, int64_t* k, int* pack_dtype) {
+    if (!w) return fail(INGOT_EINVAL, "nil weight");
+    if (n) *n = w->n;
+    if (k) *k = w->k;
+    if (pack_dtype) *pack_dtype = w->pack_dtype;
+    return INGOT_OK;
+}
+
+// ---------------- GEMM / GEMV ----------------
+
+static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
+    const ingot_rocm_weight* w = a->w;
+    const int M = (int)a->M;
+    const int64_t RB = (a->N + 63) / 64;
+    const int64_t KT = w->kp / 256;
+    if (RB > ingot_rocm_session::kCounters) return fail(INGOT_EDECLINED, "gemv: N %lld too large", (long long)a->N);
+    // K slice bound by LDS: M·(KS+8)·4 bytes of staged activations <= 64 KiB.
+    const int64_t kmax = std::max<int64_t>(256, (16384 / M - 8) / 256 * 256);
+    int64_t target = (int64_t)s->num_cus * 4;
+    if (const char* t = getenv("INGOT_GEMV_TARGET")) target = std::max(1, atoi(t));
+    int64_t S = 0;
+    for (int64_t d = 1; d <= KT; ++d) {
+        if (KT % d) continue;
+        if (w->kp / d > kmax) continue;
+        if (S == 0 || RB * d <= target) S = d;
+    }
+    if (S == 0) S = KT;
+    GemvArgs g;
+    g.x = (const float*)a->d_a;
+    g.ldx = a->lda;
+    g.M = M;
+    g.K = (int)a->K;
+    g.w = (const uint16_t*)w->data;
+    g.ldw = w->kp;
+    g.N = (int)a->N;
+    g.S = (int)S;
+    g.KS = (int)(w->kp / S);
+    g.part = nullptr;
+    g.cnt = s->counters;
+    g.epi = make_epi(a);
+    g.y = a->d_y;
+    g.ldy = a->ldy;
+    if (S > 1) {
+        void* ws;
+        int rc = ws_reserve(s, (size_t)RB * S * M * 64 * sizeof(float), &ws);
+        if (rc) return rc;
+        g.part = (float*)ws;
+    }
+    hipError_t e = launch_gemv_bf16(g, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "gemv launch");
+    return INGOT_OK;
+}
+
+static int validate_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!a || !a->w) return fail(INGOT_EINVAL, "gemm: nil arguments or weight");
+    const ingot_rocm_weight* w = a->w;
+    if (a->M < 0 || a->N != w->n || a->K != w->k)
+        return fail(INGOT_EINVAL, "gemm: shape M=%lld N=%lld K=%lld does not match weight [%lld,%lld]", (long long)a->M,
+                    (long long)a->N, (long long)a->K, (long long)w->n, (long long)w->k);
+    if (w->kind == KIND_I8) return fail(INGOT_EINVAL, "gemm: int8 weights run through ingot_rocm_matmul_integer");
+    if (a->a_dtype != INGOT_DT_F32 && a->a_dtype != INGOT_DT_BF16) return fail(INGOT_EINVAL, "gemm: A must be f32 or bf16");
+    if (a->M > 0 && (!a->d_a || !a->d_y)) return fail(INGOT_EINVAL, "gemm: nil A or Y");
+    const int64_t amin = a->trans_a ? a->M : a->K;
+    if (a->lda < amin) return fail(INGOT_EINVAL, "gemm: lda %lld < %lld", (long long)a->lda, (long long)amin);
+    if (a->ldy < a->N) return fail(INGOT_EINVAL, "gemm: ldy %lld < N %lld", (long long)a->ldy, (long long)a->N);
+    if (a->M > INT32_MAX / 2 || a->N > INT32_MAX / 2) return fail(INGOT_EINVAL, "gemm: dimension too large");
+    if (a->math == INGOT_MATH_F32 && w->kind != KIND_F32)
+        return fail(INGOT_EDECLINED, "gemm: f32 math needs an f32-packed weight");
+    if (a->math == INGOT_MATH_BF16 && w->kind != KIND_BF16)
+        return fail(INGOT_EDECLINED, "gemm: bf16 math needs a bf16-packed weight");
+    if (w->kind == KIND_F32 && a->a_dtype == INGOT_DT_BF16)
+        return fail(INGOT_EDECLINED, "gemm: bf16 activations need a bf16-packed weight");
+    return check_epi(a);
+}
+
+int ingot_rocm_gemv_bf16(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
+    int rc = validate_gemm(s, a);
+    if (rc) return rc;
+    if (a->w->kind != KIND_BF16 || a->M > 16 || a->a_dtype != INGOT_DT_F32 || a->trans_a || a->batch > 1)
+        return fail(INGOT_EINVAL, "gemv_bf16: needs M <= 16 rows of f32 A (no transA, no batch) and a bf16 weight");
+    if (a->M == 0) return INGOT_OK;
+    return run_gemv(s, a);
+}
+
+int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
+    int rc = validate_gemm(s, a);
+    if (rc) return rc;
+    const ingot_rocm_weight* w = a->w;
+    const int64_t batch = std::max<int64_t>(1, a->batch);
+    if (a->M == 0 || a->N == 0) return INGOT_OK;
+    if (w->kind == KIND_BF16 && a->M <= 16 && !a->trans_a && a->a_dtype == INGOT_DT_F32 && batch == 1 &&
+        !getenv("INGOT_NO_GEMV"))
+        return run_gemv(s, a);
+
+    const GemmKind kind = w->kind;
+    const int esz = kind_size(kind);
+    const int64_t kl = round_up(a->K, ktile_elems(kind));
+    const int a_esz = elem_size(a->a_dtype);
+    const bool a_native = (kind == KIND_BF16) == (a->a_dtype == INGOT_DT_BF16);
+    const bool direct = a_native && !a->trans_a && a->K % ktile_elems(kind) == 0 && (a->lda * a_esz) % 16 == 0 &&
+                        aligned16(a->d_a) && (batch == 1 || (a->stride_a * a_esz) % 16 == 0);
+    GemmArgs g;
+    memset(&g, 0, sizeof g);
+    if (direct) {
+        g.a = (const char*)a->d_a;
+        g.lda_bytes = a->lda * a_esz;
+        g.stride_a_bytes = a->stride_a * a_esz;
+    } else {
+        void* ws;
+        rc = ws_reserve(s, (size_t)(batch * a->M * kl * esz), &ws);
+        if (rc) return rc;
+        hipError_t e = launch_pack_a(a->d_a, a->a_dtype, a->lda, a->trans_a, a->M, a->K, a->stride_a, ws, kind, kl,
+                                     a->M * kl, (int)batch, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "pack A");
+        g.a = (const char*)ws;
+        g.lda_bytes = kl * esz;
+        g.stride_a_bytes = a->M * kl * esz;
+    }
+    g.b = (const char*)w->data;
+    g.ldb_bytes = w->kp * esz;
+    g.M = (int)a->M;
+    g.N = (int)a->N;
+    g.kt = (int)(kl * esz / KTILE_BYTES);
+    g.b_rows = (int)w->np;
+    g.stride_y = a->stride_y;
+    g.y = a->d_y;
+    g.ldy = a->ldy;
+    g.epi = make_epi(a);
+    const int cfg = pick_config(kind, a->M, a->N, batch, s->num_cus);
+    const GemmConfig* c;
+    gemm_configs(kind, &c);
+    g.tiles_m = (int)((a->M + c[cfg].bm - 1) / c[cfg].bm);
+    g.tiles_n = (int)((a->N + c[cfg].bn - 1) / c[cfg].bn);
+    hipError_t e = launch_gemm(kind, cfg, g, (int)batch, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "gemm launch");
+    return INGOT_OK;
+}
+
+int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64_t K, const void* d_a, int32_t a_dtype,
+                              int64_t lda, int32_t za, const ingot_rocm_weight* w, int32_t* d_y_i32,
+                              const float* d_dq_scale, int64_t n_scale, int32_t dq_zp, float* d_y_f32) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!w || w->kind != KIND_I8) return fail(INGOT_EINVAL, "matmul_integer: weight must be packed as int8");
+    if (N != w->n || K != w->k || M < 0)
+        return fail(INGOT_EINVAL, "matmul_integer: shape M=%lld N=%lld K=%lld does not match weight [%lld,%lld]",
+                    (long long)M, (long long)N, (long long)K, (long long)w->n, (long long)w->k);
+    if (a_dtype != INGOT_DT_U8 && a_dtype != INGOT_DT_I8) return fail(INGOT_EINVAL, "matmul_integer: A must be u8 or s8");
+    if (!d_y_i32 && !d_y_f32) return fail(INGOT_EINVAL, "matmul_integer: no output");
+    if (d_y_f32 && (!d_dq_scale || (n_scale != 1 && n_scale != N)))
+        return fail(INGOT_EINVAL, "matmul_integer: dequant scale must have 1 or N elements");
+    if (lda < K) return fail(INGOT_EINVAL, "matmul_integer: lda < K");
+    if (M == 0) return INGOT_OK;
+    if (!d_a) return fail(INGOT_EINVAL, "matmul_integer: nil A");
+    const bool u8 = a_dtype == INGOT_DT_U8;
+    const int32_t za_s8 = u8 ? za - 128 : za;
+    const int64_t kl = round_up(K, 128);
+    const bool direct = K % 128 == 0 && lda % 16 == 0 && aligned16(d_a);
+    GemmArgs g;
+    memset(&g, 0, sizeof g);
+    if (direct) {
+        g.a = (const char*)d_a;
+        g.lda_bytes = lda;
+        g.a_xor = u8 ? 1 : 0;
+    } else {
+        void* ws;
+        rc = ws_reserve(s, (size_t)(M * kl), &ws);
+        if (rc) return rc;
+        hipError_t e = launch_pack_a(d_a, a_dtype, lda, 0, M, K, 0, ws, KIND_I8, kl, 0, 1, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "pack A");
+        g.a = (const char*)ws;
+        g.lda_bytes = kl;
+    }
+    g.b = (const char*)w->data;
+    g.ldb_bytes = w->kp;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.kt = (int)(kl / KTILE_BYTES);
+    g.b_rows = (int)w->np;
+    g.ldy = N;
+    g.qepi.colsum = w->colsum;
+    g.qepi.neg_za = (int32_t)(0u - (uint32_t)za_s8);
+    g.qepi.yi = d_y_i32;
+    g.qepi.yf = d_y_f32;
+    g.qepi.scale = d_dq_scale;
+    g.qepi.n_scale = n_scale;
+    g.qepi.dq_zp = dq_zp;
+    const int cfg = pick_config(KIND_I8, M, N, 1, s->num_cus);
+    const GemmConfig* c;
+    gemm_configs(KIND_I8, &c);
+    g.tiles_m = (int)((M + c[cfg].bm - 1) / c[cfg].bm);
+    g.tiles_n = (int)((N + c[cfg].bn - 1) / c[cfg].bn);
+    hipError_t e = launch_gemm(KIND_I8, cfg, g, 1, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "qgemm launch");
+    return INGOT_OK;
+}
+
+int ingot_rocm_dequantize_linear(ingot_rocm_session* s, const void* d_x, int32_t x_dtype, int64_t n,
+                                 const float* d_scale, int64_t n_scale, int64_t inner, const void* d_zp,
+                                 int32_t zp_dtype, int64_t n_zp, float* d_y) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (x_dtype != INGOT_DT_U8 && x_dtype != INGOT_DT_I8 && x_dtype != INGOT_DT_I32)
+        return fail(INGOT_EINVAL, "dequantize_linear: unsupported input dtype %d", x_dtype);
+    if (d_zp && zp_dtype != INGOT_DT_U8 && zp_dtype != INGOT_DT_I8 && zp_dtype != INGOT_DT_I32)
+        return fail(INGOT_EINVAL, "dequantize_linear: unsupported zero_point dtype %d", zp_dtype);
+    if (n_scale < 1 || (d_zp && n_zp != 1 && n_zp != n_scale))
+        return fail(INGOT_EINVAL, "dequantize_linear: scale/zero_point sizes %lld/%lld", (long long)n_scale, (long long)n_zp);
+    if (n == 0) return INGOT_OK;
+    if (!d_x || !d_scale || !d_y) return fail(INGOT_EINVAL, "dequantize_linear: nil pointer");
+    hipError_t e = launch_dequant(d_x, x_dtype, n, d_scale, n_scale, inner, d_zp, zp_dtype, n_zp, d_y, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return INGOT_OK;
+}
+
+int ingot_rocm_activation(ingot_rocm_session* s, const float* d_x, float* d_y, int64_t rows, int64_t cols,
+                          const float* d_bias, int32_t act, float act_alpha, float act_beta, int32_t post,
+                          float post_scale, float post_shift) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (act < INGOT_ACT_NONE || act > INGOT_ACT_LEAKYRELU) return fail(INGOT_EINVAL, "unknown activation %d", act);
+    if (rows < 0 || cols < 0) return fail(INGOT_EINVAL, "negative size");
+    if (rows * cols == 0) return INGOT_OK;
+    if (!d_x || !d_y) return fail(INGOT_EINVAL, "nil pointer");
+    hipError_t e = launch_activation(d_x, d_y, rows, cols, d_bias, act, act_alpha, act_beta, post, post_scale,
+                                     post_shift, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "activation launch");
+    return INGOT_OK;
+}
+
+int ingot_rocm_cast_bf16(ingot_rocm_session* s, const float* d_x, uint16_t* d_y, int64_t n) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (n == 0) return INGOT_OK;
+    if (!d_x || !d_y || n < 0) return fail(INGOT_EINVAL, "cast_bf16: bad arguments");
+    hipError_t e = launch_cast_bf16(d_x, d_y, n, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "cast launch");
+    return INGOT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,43 @@
+// Session and weight objects shared by runtime.cpp and ops.cpp.
+#pragma once
+
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "kernels.hpp"
+
+struct ingot_rocm_weight {
+    int pack_dtype;          // INGOT_DT_F32 / BF16 / I8
+    ingot::GemmKind kind;
+    int64_t n, k;            // logical [n][k]
+    int64_t np, kp;          // packed [np][kp], zero padded to multiples of 256
+    void* data;
+    int32_t* colsum;         // int8 weights: Σ_k W[n][k]
+};
+
+struct ingot_rocm_session {
+    static constexpr int64_t kCounters = 1 << 16;  // split-K arrival counters
+    int device = 0;
+    int num_cus = 256;
+    hipStream_t stream = nullptr;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    void* ws = nullptr;  // workspace: packed activations, split-K partials
+    size_t ws_bytes = 0;
+    unsigned* counters = nullptr;
+    std::vector<ingot_rocm_weight*> weights;
+    std::map<size_t, std::vector<void*>> free_bufs;    // pool: size class → free buffers
+    std::unordered_map<void*, size_t> buf_class;       // pool: buffer → size class
+};
+
+namespace ingot {
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t e, const char* what);
+int session_enter(ingot_rocm_session* s);
+int ws_reserve(ingot_rocm_session* s, size_t bytes, void** out);
+void* pool_get(ingot_rocm_session* s, size_t bytes);
+void pool_put(ingot_rocm_session* s, void* p);
+
+}  // namespace ingot

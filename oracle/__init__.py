@@ -1,0 +1,219 @@
+"""CPU oracle of ingot's dense-contraction hot path (TEST INFRASTRUCTURE ONLY).
+
+Loads oracle/liboracle.so (oracle.c: scalar restatements of the reference's
+Go functions, each citing its file:line) and oracle/libbaseline.so
+(baseline.cpp: the reference's threaded amd64 GEMM algorithm, restated in
+C++, for bench.py's cpu_baseline). Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg import this package, and only as the checker.
+
+Parity pinning: every function here is checked in tests/test_oracle.py
+against the reference tests' known answers (tests/golden/kats.json) and
+independent closed forms; see that file's docstring for the mapping.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+F32, BF16, I8, U8, I32 = 1, 3, 4, 5, 7
+
+_P = C.c_void_p
+_I64 = C.c_int64
+
+_orc = None
+_base = None
+
+
+def _load(name: str) -> C.CDLL:
+    path = os.path.join(HERE, name)
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} missing: run `make -C oracle`")
+    return C.CDLL(path)
+
+
+def lib() -> C.CDLL:
+    global _orc
+    if _orc is None:
+        L = _load("liboracle.so")
+        L.orc_f32_to_bf16.restype = C.c_uint16
+        L.orc_f32_to_bf16.argtypes = [C.c_float]
+        L.orc_bf16_to_f32.restype = C.c_float
+        L.orc_bf16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_bf16_n.argtypes = [_P, _P, _I64]
+        L.orc_act.restype = C.c_double
+        L.orc_act.argtypes = [C.c_double, C.c_int, C.c_double, C.c_double]
+        L.orc_gemm_ref_f32.argtypes = [_I64, _I64, _I64, C.c_float, _P, _I64, _P, _I64, C.c_float, _P, _I64]
+        L.orc_gemm.restype = C.c_int
+        L.orc_gemm.argtypes = [_I64, _I64, _I64, _P, _I64, C.c_int, _P, C.c_int, _I64, C.c_int, C.c_float, C.c_float,
+                               _P, C.c_int, _I64, C.c_int, C.c_float, C.c_float, C.c_int, C.c_float, C.c_float, _P]
+        L.orc_dot_bf16.restype = C.c_float
+        L.orc_dot_bf16.argtypes = [_P, _P, _I64]
+        L.orc_gemv_bf16.argtypes = [_I64, _I64, _P, _P, _I64, _P]
+        L.orc_qgemm_ref.argtypes = [_I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64]
+        L.orc_matmul_integer.argtypes = [_I64, _I64, _I64, _P, C.c_int, C.c_int32, _P, _P]
+        L.orc_matmul_integer_shifted.argtypes = [_I64, _I64, _I64, _P, C.c_int, C.c_int32, _P, _P]
+        L.orc_dequantize_linear.argtypes = [_P, C.c_int, _I64, _P, _I64, _I64, _P, C.c_int, _I64, _P]
+        _orc = L
+    return _orc
+
+
+def baseline() -> C.CDLL:
+    global _base
+    if _base is None:
+        B = _load("libbaseline.so")
+        B.base_pack_b_f32.restype = _P
+        B.base_pack_b_f32.argtypes = [_I64, _I64, _P, _I64, C.c_int]
+        B.base_pack_b_bf16.restype = _P
+        B.base_pack_b_bf16.argtypes = [_I64, _I64, _P, _I64, C.c_int]
+        B.base_free_packed.argtypes = [_P]
+        B.base_sgemm_packed.argtypes = [_I64, _P, _I64, _P, _P, _I64, _P, C.c_int, C.c_int]
+        B.base_gemv_bf16.argtypes = [_I64, _I64, _I64, _P, _P, _P, C.c_int]
+        B.base_qgemm.argtypes = [_I64, _I64, _I64, _P, C.c_int32, _P, _P, C.c_int]
+        _base = B
+    return _base
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+# ---------------- restatements ----------------
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """F32ToBF16 (kernels/gemm/bgemm.go:20-26) elementwise."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_bf16_n(_p(x), _p(y), x.size)
+    return y
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint32) << 16).view(np.float32)
+
+
+def act(x: float, code: int, a: float = 0.0, b: float = 0.0) -> float:
+    return lib().orc_act(x, code, a, b)
+
+
+def gemm_ref_f32(a, b, alpha=1.0, beta=0.0, c=None):
+    """Ref (kernels/gemm/ref.go:4-18): C = alpha·A·B + beta·C, f32 accumulation."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    m, k = a.shape
+    n = b.shape[1]
+    out = np.zeros((m, n), np.float32) if c is None else np.array(c, np.float32, order="C", copy=True)
+    lib().orc_gemm_ref_f32(m, n, k, alpha, _p(a), k, _p(b), n, beta, _p(out), n)
+    return out
+
+
+def gemm(a, b, *, trans_a=False, trans_b=False, b_dtype=F32, alpha=1.0, beta=0.0, c=None, c_mode=0, ldc=0,
+         act_code=0, act_alpha=0.0, act_beta=0.0, post=False, post_scale=1.0, post_shift=0.0) -> np.ndarray:
+    """The Gemm op (ops/matmul.go:27-139) + epilogue, float64 accumulation."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.uint16 if b_dtype == BF16 else np.float32)
+    M, K = (a.shape[1], a.shape[0]) if trans_a else a.shape
+    N = b.shape[0] if trans_b else b.shape[1]
+    y = np.empty((M, N), np.float64)
+    cc = None if c is None else np.ascontiguousarray(c, np.float32)
+    rc = lib().orc_gemm(M, N, K, _p(a), a.shape[1], int(trans_a), _p(b), b_dtype, b.shape[1], int(trans_b), alpha,
+                        beta, _p(cc), c_mode, ldc, act_code, act_alpha, act_beta, int(post), post_scale, post_shift,
+                        _p(y))
+    if rc:
+        raise ValueError("orc_gemm: bad arguments")
+    return y
+
+
+def gemv_bf16(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """GemvBF16 per row (kernels/gemm/bgemm.go:201-206), sequential f32 dots."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.uint16)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    for i in range(m):
+        lib().orc_gemv_bf16(n, k, _p(x[i]), _p(w), k, _p(y[i]))
+    return y
+
+
+def qgemm_ref(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """QgemmRef (kernels/gemm/qgemm.go:173-183)."""
+    a = np.ascontiguousarray(a, np.uint8)
+    b = np.ascontiguousarray(b, np.int8)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.int32)
+    lib().orc_qgemm_ref(m, n, k, _p(a), k, _p(b), n, _p(c), n)
+    return c
+
+
+def matmul_integer(a: np.ndarray, b: np.ndarray, za: int, shifted: bool = False) -> np.ndarray:
+    """MatMulInteger (ops/quant.go:831-900): closed form, or the reference's u8→s8 route."""
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b, np.int8)
+    m, k = a.shape
+    n = b.shape[1]
+    y = np.empty((m, n), np.int32)
+    fn = lib().orc_matmul_integer_shifted if shifted else lib().orc_matmul_integer
+    fn(m, n, k, _p(a), U8 if a.dtype == np.uint8 else I8, za, _p(b), _p(y))
+    return y
+
+
+def dequantize_linear(x: np.ndarray, scale: np.ndarray, inner: int = 1, zp: np.ndarray = None) -> np.ndarray:
+    """DequantizeLinear (ops/quant.go:173-229)."""
+    x = np.ascontiguousarray(x)
+    scale = np.ascontiguousarray(scale, np.float32)
+    dt = {np.dtype(np.uint8): U8, np.dtype(np.int8): I8, np.dtype(np.int32): I32}[x.dtype]
+    zdt = 0 if zp is None else {np.dtype(np.uint8): U8, np.dtype(np.int8): I8, np.dtype(np.int32): I32}[zp.dtype]
+    y = np.empty(x.shape, np.float32)
+    lib().orc_dequantize_linear(_p(x), dt, x.size, _p(scale), scale.size, inner, _p(zp), zdt,
+                                1 if zp is None else zp.size, _p(y))
+    return y
+
+
+# ---------------- threaded CPU baseline (bench.py's cpu_baseline leg) ----------------
+
+class PackedB:
+    """A weight packed once for base_sgemm_packed (PackB / PackBBF16)."""
+
+    def __init__(self, w: np.ndarray, trans_b: bool, bf16: bool):
+        self.k, self.n = (w.shape[1], w.shape[0]) if trans_b else w.shape
+        self._w = np.ascontiguousarray(w)
+        fn = baseline().base_pack_b_bf16 if bf16 else baseline().base_pack_b_f32
+        self.h = fn(self.k, self.n, _p(self._w), self._w.shape[1], int(trans_b))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            baseline().base_free_packed(self.h)
+            self.h = None
+
+
+def base_sgemm(a: np.ndarray, pb: PackedB, bias=None, gelu=False, threads=1, out=None) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    m = a.shape[0]
+    y = np.empty((m, pb.n), np.float32) if out is None else out
+    bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    baseline().base_sgemm_packed(m, _p(a), a.shape[1], pb.h, _p(y), pb.n, _p(bb), int(gelu), threads)
+    return y
+
+
+def base_gemv_bf16(x: np.ndarray, w: np.ndarray, threads=1) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.uint16)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    baseline().base_gemv_bf16(m, k, n, _p(x), _p(w), _p(y), threads)
+    return y
+
+
+def base_qgemm(a: np.ndarray, bt: np.ndarray, za: int, threads=1) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.uint8)
+    bt = np.ascontiguousarray(bt, np.int8)
+    m, k = a.shape
+    n = bt.shape[0]
+    y = np.empty((m, n), np.int32)
+    baseline().base_qgemm(m, n, k, _p(a), za, _p(bt), _p(y), threads)
+    return y

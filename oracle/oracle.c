@@ -1,0 +1,199 @@
+/*
+ * oracle.c — CPU restatement of ingot's dense-contraction hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker for the GPU kernels,
+ * never part of the product.
+ *
+ * Pinning (tests/test_oracle.py): the reference's known-answer tests
+ * (TestGemmTransB ops/compute_optest_test.go:232-252, TestMatMulBatched
+ * :254-274, TestDequantizeLinear ops/quant_optest_test.go:60-73,
+ * TestQLinearMatMulAndMatMulInteger :194-223), closed forms (RNE bit
+ * patterns of F32ToBF16, erf/tanh identities, exact small-integer products)
+ * and independent implementations (numpy float64 matmul, brute-force int64).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <string.h>
+
+/* F32ToBF16 (kernels/gemm/bgemm.go:20-26): RNE, NaN kept quiet. */
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((b >> 16) | 0x40u);
+    return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+
+/* BF16ToF32 (kernels/gemm/bgemm.go:28-29). */
+float orc_bf16_to_f32(uint16_t h) {
+    uint32_t b = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+void orc_f32_to_bf16_n(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_f32_to_bf16(x[i]);
+}
+
+/* expScalar's clamp (kernels/vek/scalar.go:7-13). */
+static double exp_clamped(double x) {
+    const double lo = -87.33654, hi = 88.37626;
+    if (x < lo) x = lo;
+    if (x > hi) x = hi;
+    return exp(x);
+}
+
+static double clamp01(double x) { return x < 0 ? 0 : (x > 1 ? 1 : x); }
+
+/* Activations of the epilogue set: ops/epilogue.go:48-73 with the generics
+ * of kernels/vek/vek_generic.go:48-76 (relu, hardswish, hardsigmoid, clip,
+ * leakyrelu), :121-125 (sigmoid), :150-155 (silu), :165-170 (gelu erf) and
+ * geluTanh (ops/elementwise.go:411-414). */
+double orc_act(double x, int act, double a, double b) {
+    switch (act) {
+        case ORC_ACT_RELU: return x > 0 ? x : 0;
+        case ORC_ACT_GELU_ERF: return 0.5 * x * (1 + erf(x / sqrt(2.0)));
+        case ORC_ACT_GELU_TANH: return 0.5 * x * (1 + tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)));
+        case ORC_ACT_SIGMOID: return 1 / (1 + exp_clamped(-x));
+        case ORC_ACT_SILU: return x / (1 + exp_clamped(-x));
+        case ORC_ACT_HARDSWISH: return x * clamp01(x / 6 + 0.5);
+        case ORC_ACT_HARDSIGMOID: return clamp01(a * x + b);
+        case ORC_ACT_CLIP: return x < a ? a : (x > b ? b : x);
+        case ORC_ACT_LEAKYRELU: return x < 0 ? x * a : x;
+        default: return x;
+    }
+}
+
+/* Ref (kernels/gemm/ref.go:4-18): f32 accumulation in k order. */
+void orc_gemm_ref_f32(int64_t m, int64_t n, int64_t k, float alpha, const float* a, int64_t lda, const float* b,
+                      int64_t ldb, float beta, float* c, int64_t ldc) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            float acc = 0;
+            for (int64_t p = 0; p < k; ++p) acc += a[i * lda + p] * b[p * ldb + j];
+            if (beta == 0) c[i * ldc + j] = alpha * acc;
+            else c[i * ldc + j] = alpha * acc + beta * c[i * ldc + j];
+        }
+}
+
+/* The Gemm op (ops/matmul.go:27-139) in float64: Y = post_scale·act(
+ * alpha·op(A)·op(B) + beta·C) + post_shift, C broadcast by the rules of
+ * ops/matmul.go:50-76, B f32 or bf16 bits (widened exactly). The float64
+ * accumulation is the oracle form of kernels/gemm/gemm_test.go:19-31. */
+int orc_gemm(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, int transA, const void* B, int b_dtype,
+             int64_t ldb, int transB, float alpha, float beta, const float* C, int c_mode, int64_t ldc, int act,
+             float act_alpha, float act_beta, int post, float post_scale, float post_shift, double* Y) {
+    if (b_dtype != ORC_F32 && b_dtype != ORC_BF16) return 1;
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = 0; j < N; ++j) {
+            double acc = 0;
+            for (int64_t p = 0; p < K; ++p) {
+                const double av = transA ? A[p * lda + i] : A[i * lda + p];
+                const int64_t bi = transB ? j * ldb + p : p * ldb + j;
+                const double bv = b_dtype == ORC_F32 ? ((const float*)B)[bi] : orc_bf16_to_f32(((const uint16_t*)B)[bi]);
+                acc += av * bv;
+            }
+            double v = (double)alpha * acc;
+            if (C && beta != 0) {
+                double c = 0;
+                switch (c_mode) {
+                    case ORC_C_FULL: c = C[i * ldc + j]; break;
+                    case ORC_C_ROW: c = C[j]; break;
+                    case ORC_C_COL: c = C[i]; break;
+                    case ORC_C_SCALAR: c = C[0]; break;
+                    default: break;
+                }
+                v += (double)beta * c;
+            }
+            v = orc_act(v, act, act_alpha, act_beta);
+            if (post) v = v * post_scale + post_shift;
+            Y[i * N + j] = v;
+        }
+    return 0;
+}
+
+/* vek.DotBF16 generic form (kernels/vek/vek_generic.go:183-190): sequential f32. */
+float orc_dot_bf16(const float* a, const uint16_t* b, int64_t n) {
+    float s = 0;
+    for (int64_t i = 0; i < n; ++i) s += a[i] * orc_bf16_to_f32(b[i]);
+    return s;
+}
+
+/* GemvBF16 (kernels/gemm/bgemm.go:201-206): y[j] = DotBF16(x, W[j]). */
+void orc_gemv_bf16(int64_t n, int64_t k, const float* x, const uint16_t* w, int64_t ldw, float* y) {
+    for (int64_t j = 0; j < n; ++j) y[j] = orc_dot_bf16(x, w + j * ldw, k);
+}
+
+/* QgemmRef (kernels/gemm/qgemm.go:173-183): u8 × s8 → exact int32. */
+void orc_qgemm_ref(int64_t m, int64_t n, int64_t k, const uint8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                   int32_t* c, int64_t ldc) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            uint32_t s = 0;
+            for (int64_t p = 0; p < k; ++p) s += (uint32_t)((int32_t)a[i * lda + p] * (int32_t)b[p * ldb + j]);
+            c[i * ldc + j] = (int32_t)s;
+        }
+}
+
+static int32_t a_at(const void* A, int a_dtype, int64_t i) {
+    return a_dtype == ORC_U8 ? (int32_t)((const uint8_t*)A)[i] : (int32_t)((const int8_t*)A)[i];
+}
+
+/* MatMulInteger semantics, closed form: Y[i,j] = Σ_p (A[i,p] − za)·B[p,j]
+ * (the expectation of TestQLinearMatMulAndMatMulInteger,
+ * ops/quant_optest_test.go:202-211), int32 wrap-around. */
+void orc_matmul_integer(int64_t M, int64_t N, int64_t K, const void* A, int a_dtype, int32_t za, const int8_t* B,
+                        int32_t* Y) {
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = 0; j < N; ++j) {
+            uint32_t s = 0;
+            for (int64_t p = 0; p < K; ++p)
+                s += (uint32_t)(a_at(A, a_dtype, i * K + p) - za) * (uint32_t)(int32_t)B[p * N + j];
+            Y[i * N + j] = (int32_t)s;
+        }
+}
+
+/* The reference's route (ops/quant.go:308-321, 803-829, 868-900): u8 → s8
+ * by ^0x80 with za′ = za − 128, the s8 product, then + (−za′)·colSum[j]. */
+void orc_matmul_integer_shifted(int64_t M, int64_t N, int64_t K, const void* A, int a_dtype, int32_t za,
+                                const int8_t* B, int32_t* Y) {
+    const int u8 = a_dtype == ORC_U8;
+    const int32_t zs = u8 ? za - 128 : za;
+    for (int64_t j = 0; j < N; ++j) {
+        uint32_t cs = 0;
+        for (int64_t p = 0; p < K; ++p) cs += (uint32_t)(int32_t)B[p * N + j];
+        const uint32_t corr = (uint32_t)(-zs) * cs;
+        for (int64_t i = 0; i < M; ++i) {
+            uint32_t s = 0;
+            for (int64_t p = 0; p < K; ++p) {
+                int32_t av = u8 ? (int32_t)(int8_t)(((const uint8_t*)A)[i * K + p] ^ 0x80) : a_at(A, a_dtype, i * K + p);
+                s += (uint32_t)(av * (int32_t)B[p * N + j]);
+            }
+            Y[i * N + j] = (int32_t)(s + corr);
+        }
+    }
+}
+
+static int32_t int_at(const void* p, int dt, int64_t i) {
+    switch (dt) {
+        case ORC_U8: return ((const uint8_t*)p)[i];
+        case ORC_I8: return ((const int8_t*)p)[i];
+        case ORC_I32: return ((const int32_t*)p)[i];
+    }
+    return 0;
+}
+
+/* DequantizeLinear (ops/quant.go:173-229): y = float32(x − z)·scale[c],
+ * c = (i / inner) % n_scale; per-tensor uses zp[0]. Two f32 roundings, so
+ * this is bit-exact to the reference. */
+void orc_dequantize_linear(const void* x, int x_dtype, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
+                           const void* zp, int zp_dtype, int64_t n_zp, float* y) {
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t c = n_scale == 1 ? 0 : (i / inner) % n_scale;
+        int32_t z = 0;
+        if (zp) z = int_at(zp, zp_dtype, n_zp > 1 ? c : 0);
+        const int32_t d = (int32_t)((uint32_t)int_at(x, x_dtype, i) - (uint32_t)z);
+        y[i] = (float)d * scale[c];
+    }
+}

@@ -1,0 +1,79 @@
+/*
+ * oracle.h — CPU restatement of ingot's dense-contraction hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it, and only as the checker. The
+ * product (libingot_rocm.so) never links or calls it.
+ *
+ * The reference (github.com/giraffesyo/ingot, Go 1.27.3) cannot be built in
+ * this image (no Go toolchain), so these functions restate its algorithms in
+ * C from the Go sources; each cites the file:line it follows. Floating-point
+ * functions accumulate in double (the float64 oracle form of the reference's
+ * own tests, kernels/gemm/gemm_test.go:19-31) unless they restate an f32
+ * routine bit for bit (orc_gemm_ref_f32, orc_dot_bf16, orc_dequantize_linear,
+ * orc_f32_to_bf16); integer functions are exact with int32 wrap-around.
+ */
+#ifndef INGOT_ORACLE_H
+#define INGOT_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes: tensor/dtype.go:12-23 */
+#define ORC_F32 1
+#define ORC_BF16 3
+#define ORC_I8 4
+#define ORC_U8 5
+#define ORC_I32 7
+
+/* activation codes (same values as INGOT_ACT_* in include/ingot_rocm.h) */
+#define ORC_ACT_NONE 0
+#define ORC_ACT_RELU 1
+#define ORC_ACT_GELU_ERF 2
+#define ORC_ACT_GELU_TANH 3
+#define ORC_ACT_SIGMOID 4
+#define ORC_ACT_SILU 5
+#define ORC_ACT_HARDSWISH 6
+#define ORC_ACT_HARDSIGMOID 7
+#define ORC_ACT_CLIP 8
+#define ORC_ACT_LEAKYRELU 9
+
+/* C broadcast modes (INGOT_C_*) */
+#define ORC_C_NONE 0
+#define ORC_C_FULL 1
+#define ORC_C_ROW 2
+#define ORC_C_COL 3
+#define ORC_C_SCALAR 4
+
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t h);
+void orc_f32_to_bf16_n(const float* x, uint16_t* y, int64_t n);
+
+double orc_act(double x, int act, double a, double b);
+
+void orc_gemm_ref_f32(int64_t m, int64_t n, int64_t k, float alpha, const float* a, int64_t lda, const float* b,
+                      int64_t ldb, float beta, float* c, int64_t ldc);
+
+int orc_gemm(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, int transA, const void* B, int b_dtype,
+             int64_t ldb, int transB, float alpha, float beta, const float* C, int c_mode, int64_t ldc, int act,
+             float act_alpha, float act_beta, int post, float post_scale, float post_shift, double* Y);
+
+float orc_dot_bf16(const float* a, const uint16_t* b, int64_t n);
+void orc_gemv_bf16(int64_t n, int64_t k, const float* x, const uint16_t* w, int64_t ldw, float* y);
+
+void orc_qgemm_ref(int64_t m, int64_t n, int64_t k, const uint8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                   int32_t* c, int64_t ldc);
+void orc_matmul_integer(int64_t M, int64_t N, int64_t K, const void* A, int a_dtype, int32_t za, const int8_t* B,
+                        int32_t* Y);
+void orc_matmul_integer_shifted(int64_t M, int64_t N, int64_t K, const void* A, int a_dtype, int32_t za,
+                                const int8_t* B, int32_t* Y);
+
+void orc_dequantize_linear(const void* x, int x_dtype, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
+                           const void* zp, int zp_dtype, int64_t n_zp, float* y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,239 @@
+"""GPU parity of the MFMA GEMM and the decode GEMV (kernel layer, C ABI).
+
+Every case compares libingot_rocm.so with the CPU oracle (float64) on the
+same seeded inputs. Bound: max-abs error <=
+1e-3·sqrt(K)·max|A|·max|B| for f32, bf16 and fused-epilogue outputs. The f32
+MFMA path is additionally held to the reference's own f32 tolerance
+(relative 1e-5·sqrt(K), kernels/gemm/gemm_test.go:34).
+Full-size configs check a sampled subset of rows against the oracle (rows
+are independent) plus run-to-run bit identity.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import announce, assert_close, bf16_weights, nstar_tol
+from ingot_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1, 1), (3, 5, 7), (4, 4, 4), (37, 29, 300), (64, 33, 129), (257, 129, 33), (130, 600, 96),
+          (300, 17, 1), (1, 200, 64), (200, 1, 64)]
+
+
+def run_gemm(sess, a, w, M, **kw):
+    y = sess.empty(L.DT_F32, (M, w.n))
+    sess.gemm(a, w, y, M, **kw)
+    return y.numpy()
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_gemm_f32_weights(sess, m, n, k):
+    announce(f"gemm f32 m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 7919 + n * 31 + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    da = sess.to_device(a)
+    w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_F32)
+    got = run_gemm(sess, da, w, m)
+    want = oracle.gemm(a, bt, trans_b=True)
+    assert_close(got, want, nstar_tol(k, a, bt), f"f32 {m}x{n}x{k}")
+    rel = np.max(np.abs(got - want) / np.maximum(np.abs(want), 1.0))
+    assert rel <= 1e-5 * math.sqrt(k), f"f32 relative error {rel:.3e}"
+    # the [K,N] source layout (MatMul / Gemm transB=0) packs to the same product
+    w2 = sess.upload_weight(np.ascontiguousarray(bt.T), trans=False, pack_dtype=L.DT_F32)
+    assert np.array_equal(run_gemm(sess, da, w2, m), got)
+    w.free(), w2.free(), da.free()
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_gemm_bf16_weights(sess, m, n, k):
+    announce(f"gemm bf16 m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 131 + n * 17 + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k))
+    da = sess.to_device(a)
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    got = run_gemm(sess, da, w, m)
+    want = oracle.gemm(a, wb, trans_b=True, b_dtype=oracle.BF16)
+    assert_close(got, want, nstar_tol(k, a, oracle.bf16_to_f32(wb)), f"bf16 {m}x{n}x{k}")
+    w.free(), da.free()
+
+
+@pytest.mark.parametrize("mode", [L.C_FULL, L.C_ROW, L.C_COL, L.C_SCALAR])
+@pytest.mark.parametrize("pack", [L.DT_F32, L.DT_BF16])
+def test_gemm_alpha_beta_c_modes(sess, mode, pack):
+    announce(f"gemm C mode {mode} pack {pack}")
+    rng = np.random.default_rng(100 + mode * 10 + pack)
+    m, n, k = 45, 70, 130
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    c = {L.C_FULL: rng.normal(size=(m, n)), L.C_ROW: rng.normal(size=n), L.C_COL: rng.normal(size=(m, 1)),
+         L.C_SCALAR: np.array([0.75])}[mode].astype(np.float32)
+    w = sess.upload_weight(bt, trans=True, pack_dtype=pack)
+    got = run_gemm(sess, sess.to_device(a), w, m, alpha=0.5, beta=-2.0, c=sess.to_device(c), c_mode=mode, ldc=n)
+    bw = bt if pack == L.DT_F32 else oracle.bf16_to_f32(oracle.f32_to_bf16(bt))
+    want = oracle.gemm(a, bw, trans_b=True, alpha=0.5, beta=-2.0, c=c, c_mode=mode, ldc=n)
+    assert_close(got, want, nstar_tol(k, a, bw) + 1e-6, f"C mode {mode}")
+
+
+@pytest.mark.parametrize("act,aa,ab", [(L.ACT_RELU, 0, 0), (L.ACT_GELU_ERF, 0, 0), (L.ACT_GELU_TANH, 0, 0),
+                                       (L.ACT_SIGMOID, 0, 0), (L.ACT_SILU, 0, 0), (L.ACT_HARDSWISH, 0, 0),
+                                       (L.ACT_HARDSIGMOID, 0.2, 0.5), (L.ACT_CLIP, -0.5, 0.7),
+                                       (L.ACT_LEAKYRELU, 0.01, 0)])
+@pytest.mark.parametrize("m", [3, 40])
+def test_gemm_fused_epilogue(sess, act, aa, ab, m):
+    """bias + activation + post scale/shift fused into the store (SgemmPackedBEpi / GemmEp)."""
+    announce(f"epilogue act={act} m={m}")
+    rng = np.random.default_rng(act * 100 + m)
+    n, k = 96, 200
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    for pack in (L.DT_F32, L.DT_BF16):
+        w = sess.upload_weight(bt, trans=True, pack_dtype=pack)
+        got = run_gemm(sess, sess.to_device(a), w, m, beta=1.0, c=sess.to_device(bias), c_mode=L.C_ROW, act=act,
+                       act_alpha=aa, act_beta=ab, post=True, post_scale=1.5, post_shift=-0.25)
+        bw = bt if pack == L.DT_F32 else oracle.bf16_to_f32(oracle.f32_to_bf16(bt))
+        want = oracle.gemm(a, bw, trans_b=True, beta=1.0, c=bias, c_mode=2, act_code=act, act_alpha=aa,
+                           act_beta=ab, post=True, post_scale=1.5, post_shift=-0.25)
+        assert_close(got, want, 1.5 * nstar_tol(k, a, bw) + 1e-5, f"act {act} pack {pack}")
+        w.free()
+
+
+def test_gemm_trans_a_and_bf16_activations(sess):
+    announce("gemm transA / bf16 A")
+    rng = np.random.default_rng(77)
+    m, n, k = 50, 66, 140
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_F32)
+    got = run_gemm(sess, sess.to_device(np.ascontiguousarray(a.T)), w, m, trans_a=True, lda=m)
+    assert_close(got, oracle.gemm(a, bt, trans_b=True), nstar_tol(k, a, bt), "transA f32")
+    wb = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_BF16)
+    a16 = oracle.f32_to_bf16(a)
+    got = run_gemm(sess, sess.to_device(a16, L.DT_BF16), wb, m, a_dtype=L.DT_BF16)
+    want = oracle.gemm(oracle.bf16_to_f32(a16), oracle.f32_to_bf16(bt), trans_b=True, b_dtype=oracle.BF16)
+    assert_close(got, want, nstar_tol(k, a, bt), "bf16 A")
+
+
+def test_gemm_batched_strided(sess):
+    announce("gemm batched")
+    rng = np.random.default_rng(78)
+    bsz, m, n, k = 3, 20, 40, 64
+    a = rng.uniform(-1, 1, (bsz, m, k)).astype(np.float32)
+    bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_F32)
+    y = sess.empty(L.DT_F32, (bsz, m, n))
+    sess.gemm(sess.to_device(a), w, y, m, batch=bsz, stride_a=m * k, stride_y=m * n)
+    got = y.numpy()
+    for i in range(bsz):
+        assert_close(got[i], oracle.gemm(a[i], bt, trans_b=True), nstar_tol(k, a, bt), f"batch {i}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 7, 16])
+@pytest.mark.parametrize("n,k", [(64, 256), (200, 300), (2048, 2048), (1000, 5632)])
+def test_gemv_bf16_decode(sess, m, n, k):
+    announce(f"gemv m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 1000 + n + k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    dx = sess.to_device(x)
+    y = sess.empty(L.DT_F32, (m, n))
+    sess.gemv_bf16(dx, w, y, m)
+    got = y.numpy()
+    want = oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16)
+    wide = oracle.bf16_to_f32(wb)
+    assert_close(got, want, nstar_tol(k, x, wide), f"gemv {m}x{n}x{k}")
+    # the hi/lo activation split keeps f32-level accuracy (reference f32 bound)
+    rel = np.max(np.abs(got - want)) / max(1.0, np.max(np.abs(want)))
+    assert rel <= 1e-5 * math.sqrt(k), f"gemv relative error {rel:.3e}"
+    # deterministic split-K: a second run is bit-identical
+    sess.gemv_bf16(dx, w, y, m)
+    assert np.array_equal(y.numpy(), got)
+    w.free()
+
+
+def test_gemv_epilogue(sess):
+    announce("gemv epilogue")
+    rng = np.random.default_rng(5)
+    m, n, k = 3, 300, 1024
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    y = sess.empty(L.DT_F32, (m, n))
+    sess.gemv_bf16(sess.to_device(x), w, y, m, alpha=0.5, beta=2.0, c=sess.to_device(bias), c_mode=L.C_ROW,
+                   act=L.ACT_SILU)
+    want = oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16, alpha=0.5, beta=2.0, c=bias, c_mode=2,
+                       act_code=L.ACT_SILU)
+    assert_close(y.numpy(), want, nstar_tol(k, x, oracle.bf16_to_f32(wb)), "gemv epilogue")
+
+
+# ---------------- BASELINE configs at full size ----------------
+
+def test_config1_gemm_relu(sess):
+    """Y = ReLU(A·Bᵀ + bias), f32, A[128,256], B[512,256], transB."""
+    announce("config 1")
+    rng = np.random.default_rng(1)
+    a = rng.uniform(-1, 1, (128, 256)).astype(np.float32)
+    b = rng.uniform(-1, 1, (512, 256)).astype(np.float32)
+    bias = rng.normal(0, 0.1, 512).astype(np.float32)
+    w = sess.upload_weight(b, trans=True, pack_dtype=L.DT_F32)
+    got = run_gemm(sess, sess.to_device(a), w, 128, beta=1.0, c=sess.to_device(bias), c_mode=L.C_ROW,
+                   act=L.ACT_RELU)
+    want = oracle.gemm(a, b, trans_b=True, beta=1.0, c=bias, c_mode=2, act_code=1)
+    assert_close(got, want, nstar_tol(256, a, b), "config 1")
+
+
+BERT = [(768, 2304, 0), (768, 768, 0), (768, 3072, L.ACT_GELU_ERF), (3072, 768, 0)]
+
+
+@pytest.mark.parametrize("k,n,act", BERT)
+def test_config2_bert_f32(sess, k, n, act):
+    """BERT-base projections, M=1024, W [K,N] f32 (MatMul layout) + bias (+GELU)."""
+    announce(f"bert k={k} n={n}")
+    rng = np.random.default_rng(k + n)
+    a = rng.normal(0, 1, (1024, k)).astype(np.float32)
+    wkn = rng.normal(0, 0.02, (k, n)).astype(np.float32)
+    bias = rng.normal(0, 0.02, n).astype(np.float32)
+    w = sess.upload_weight(wkn, trans=False, pack_dtype=L.DT_F32)
+    got = run_gemm(sess, sess.to_device(a), w, 1024, beta=1.0, c=sess.to_device(bias), c_mode=L.C_ROW, act=act)
+    rows = np.arange(0, 1024, 37)
+    want = oracle.gemm(a[rows], wkn, beta=1.0, c=bias, c_mode=2, act_code=act)
+    assert_close(got[rows], want, nstar_tol(k, a, wkn), f"bert {k}x{n}")
+
+
+@pytest.mark.parametrize("k,n,act", [(3072, 9216, 0), (3072, 12288, L.ACT_GELU_ERF), (12288, 3072, 0)])
+def test_config5_dit_bf16(sess, k, n, act):
+    """DiT GEMMs, M=4096, A f32 → bf16 RNE on load, W bf16 [N,K], f32 accumulate."""
+    announce(f"dit k={k} n={n}")
+    rng = np.random.default_rng(k * 3 + n)
+    a = rng.normal(0, 1, (4096, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    da = sess.to_device(a)
+    got = run_gemm(sess, da, w, 4096, act=act)
+    rows = np.arange(5, 4096, 257)
+    want = oracle.gemm(a[rows], wb, trans_b=True, b_dtype=oracle.BF16, act_code=act)
+    assert_close(got[rows], want, nstar_tol(k, a, oracle.bf16_to_f32(wb)), f"dit {k}x{n}")
+    assert np.array_equal(run_gemm(sess, da, w, 4096, act=act), got), "run-to-run bit identity"
+    w.free(), da.free()
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("k,n", [(2048, 6144), (2048, 2048), (2048, 11264), (5632, 2048)])
+def test_config4_decode_gemv(sess, m, k, n):
+    """Llama-style decode, bf16 weights, M in {1,4,16} (Gemm op path: M <= 16 → GEMV)."""
+    announce(f"decode m={m} k={k} n={n}")
+    rng = np.random.default_rng(m + k + n)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    got = run_gemm(sess, sess.to_device(x), w, m)
+    want = oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16)
+    assert_close(got, want, nstar_tol(k, x, oracle.bf16_to_f32(wb)), f"decode {m}x{k}x{n}")
+    w.free()

@@ -1,0 +1,94 @@
+"""GPU parity of int8 MatMulInteger (+ fused DequantizeLinear) and DequantizeLinear.
+
+Bar: bit-exact. int32 outputs equal the oracle's closed form Σ(a−za)·b
+(ops/quant.go:831-900); dequantized f32 outputs equal float32(y − z)·scale
+(ops/quant.go:173-229) bit for bit.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import announce
+from ingot_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+
+KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "kats.json")))
+
+
+def test_matmul_integer_kat(sess):
+    announce("int8 kat")
+    k = KATS["matmul_integer"]
+    a = np.array(k["A"], np.uint8).reshape(k["m"], k["k"])
+    b = np.array(k["B"], np.int8).reshape(k["k"], k["n"])
+    w = sess.upload_weight(b, trans=False, pack_dtype=L.DT_I8)
+    y = sess.empty(L.DT_I32, (k["m"], k["n"]))
+    sess.matmul_integer(sess.to_device(a), w, k["m"], k["za"], y_i32=y)
+    assert np.array_equal(y.numpy(), np.array(k["Y"], np.int32))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 33, 12), (5, 128, 70), (64, 256, 64), (130, 384, 200),
+                                   (300, 100, 33)])
+@pytest.mark.parametrize("a_dt,za", [(np.uint8, 128), (np.uint8, 0), (np.uint8, 201), (np.int8, 0), (np.int8, -9)])
+def test_matmul_integer_exact(sess, m, k, n, a_dt, za):
+    announce(f"int8 m={m} k={k} n={n} a={np.dtype(a_dt).name} za={za}")
+    rng = np.random.default_rng(m * 17 + k * 3 + n + za)
+    lo, hi = (0, 256) if a_dt == np.uint8 else (-128, 128)
+    a = rng.integers(lo, hi, (m, k)).astype(a_dt)
+    b = rng.integers(-128, 128, (k, n)).astype(np.int8)
+    w = sess.upload_weight(b, trans=False, pack_dtype=L.DT_I8)
+    y = sess.empty(L.DT_I32, (m, n))
+    sess.matmul_integer(sess.to_device(a, L.DT_U8 if a_dt == np.uint8 else L.DT_I8), w, m, za, y_i32=y)
+    assert np.array_equal(y.numpy(), oracle.matmul_integer(a, b, za))
+    w.free()
+
+
+def test_config3_matmul_integer_dequant(sess):
+    """A u8 [1024,768] za=128, B s8 [768,3072] zp 0, then per-column dequant."""
+    announce("config 3 int8")
+    rng = np.random.default_rng(3)
+    a = rng.integers(0, 256, (1024, 768)).astype(np.uint8)
+    b = rng.integers(-127, 128, (768, 3072)).astype(np.int8)
+    scale = (rng.uniform(0.001, 0.01, 3072).astype(np.float32) * np.float32(0.02)).astype(np.float32)
+    w = sess.upload_weight(b, trans=False, pack_dtype=L.DT_I8)
+    da = sess.to_device(a, L.DT_U8)
+    yi = sess.empty(L.DT_I32, (1024, 3072))
+    yf = sess.empty(L.DT_F32, (1024, 3072))
+    ds = sess.to_device(scale)
+    sess.matmul_integer(da, w, 1024, 128, y_i32=yi, scale=ds, y_f32=yf)
+    want = oracle.matmul_integer(a, b, 128)
+    got_i = yi.numpy()
+    assert np.array_equal(got_i, want)
+    assert np.array_equal(yf.numpy(), oracle.dequantize_linear(want, scale, inner=1))
+    # f32-only output (the fused form) matches too
+    yf2 = sess.empty(L.DT_F32, (1024, 3072))
+    sess.matmul_integer(da, w, 1024, 128, scale=ds, y_f32=yf2)
+    assert np.array_equal(yf2.numpy(), yf.numpy())
+
+
+def test_dequantize_kats(sess):
+    announce("dequant kats")
+    for name, dt, code in [("dequantize_u8", np.uint8, L.DT_U8), ("dequantize_i8", np.int8, L.DT_I8)]:
+        k = KATS[name]
+        x = sess.to_device(np.array(k["x"], dt), code)
+        y = sess.empty(L.DT_F32, (len(k["x"]),))
+        sess.dequantize_linear(x, sess.to_device(np.array(k["scale"], np.float32)), y,
+                               zp=sess.to_device(np.array(k["zp"], dt), code))
+        assert np.array_equal(y.numpy(), np.array(k["y"], np.float32))
+
+
+@pytest.mark.parametrize("xdt,code", [(np.uint8, L.DT_U8), (np.int8, L.DT_I8), (np.int32, L.DT_I32)])
+def test_dequantize_per_axis_exact(sess, xdt, code):
+    announce(f"dequant per-axis {np.dtype(xdt).name}")
+    rng = np.random.default_rng(9)
+    info = np.iinfo(xdt)
+    x = rng.integers(max(info.min, -2**24), min(info.max, 2**24), (6, 5, 7), endpoint=True).astype(xdt)
+    sc = rng.uniform(0.001, 0.01, 5).astype(np.float32)
+    zp = rng.integers(-3, 4, 5).astype(np.int32) if xdt == np.int32 else rng.integers(0, 100, 5).astype(xdt)
+    zcode = L.DT_I32 if xdt == np.int32 else code
+    y = sess.empty(L.DT_F32, x.shape)
+    sess.dequantize_linear(sess.to_device(x, code), sess.to_device(sc), y, inner=7, zp=sess.to_device(zp, zcode))
+    assert np.array_equal(y.numpy(), oracle.dequantize_linear(x, sc, inner=7, zp=zp))

@@ -1,0 +1,209 @@
+"""The operator layer (op.Op mirror) on the GPU, case for case after the
+reference's op tests (ops/compute_optest_test.go, ops/gemm_bf16_optest_test.go,
+ops/quant_optest_test.go), checked against the CPU oracle.
+
+Exact known answers are compared bit for bit; floating-point products use the
+north-star bound 1e-3·sqrt(K)·max|A|·max|B| (and the reference's own
+1e-4 relative eqF32 bound where its test used it on exact inputs).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import announce, assert_close, bf16_weights, nstar_tol
+from ingot_amd import IngotError
+from ingot_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+
+KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "kats.json")))
+
+
+def dev(sess, arr, code=None):
+    return sess.to_device(np.ascontiguousarray(arr), code)
+
+
+def run(op, *ins):
+    outs = op.run(*ins)
+    res = [o.numpy() for o in outs]
+    for o in outs:
+        o.free()
+    return res
+
+
+def test_lookup_errors(sess):
+    with pytest.raises(IngotError, match="unsupported op"):
+        sess.op("Conv", 11)
+    with pytest.raises(IngotError, match="not supported at opset 6"):
+        sess.op("Gemm", 6)
+    with pytest.raises(IngotError, match="unknown ingot_act"):
+        sess.op("MatMul", 13, {"ingot_act": "swish"})
+
+
+def test_gemm_transb_kat(sess):
+    """TestGemmTransB (ops/compute_optest_test.go:232-252), bit-exact."""
+    announce("op gemm kat")
+    k = KATS["gemm_transb"]
+    a = np.array(k["A"], np.float32).reshape(k["A_shape"])
+    b = np.array(k["B"], np.float32).reshape(k["B_shape"])
+    c = np.array(k["C"], np.float32)
+    op = sess.op("Gemm", 7, {"transB": 1, "alpha": 2.0, "beta": 1.0})
+    (y,) = run(op, dev(sess, a), dev(sess, b), dev(sess, c))
+    assert y.shape == (2, 4)
+    assert np.array_equal(y, np.array(k["Y"], np.float32))
+
+
+def test_matmul_batched_kat(sess):
+    """TestMatMulBatched (ops/compute_optest_test.go:254-274), bit-exact."""
+    announce("op matmul batched kat")
+    k = KATS["matmul_batched"]
+    a = np.array(k["A"], np.float32).reshape(k["A_shape"])
+    b = np.array(k["B"], np.float32).reshape(k["B_shape"])
+    (y,) = run(sess.op("MatMul", 1), dev(sess, a), dev(sess, b))
+    assert np.array_equal(y, np.array(k["Y"], np.float32))
+
+
+@pytest.mark.parametrize("as_,bs", [((2, 2, 3), (3, 2)), ((7, 1, 384), (384, 96)), ((3, 5, 17), (17, 9)),
+                                    ((2, 3, 4, 33), (33, 5)), ((33,), (33, 5)), ((4, 33), (33,))])
+def test_matmul_broadcast_batch(sess, as_, bs):
+    """TestMatMulBroadcastBatch (:280-318) plus the NumPy 1-D promotions."""
+    announce(f"op matmul bcast {as_} {bs}")
+    rng = np.random.default_rng(7)
+    a = rng.uniform(-1, 1, as_).astype(np.float32)
+    b = rng.uniform(-1, 1, bs).astype(np.float32)
+    (y,) = run(sess.op("MatMul", 13), dev(sess, a), dev(sess, b))
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64))
+    assert y.shape == want.shape
+    assert_close(y, want, nstar_tol(bs[0], a, b), "matmul bcast")
+
+
+@pytest.mark.parametrize("as_,bs", [((128, 384), (384, 1152)), ((1, 16, 48), (48, 144)), ((7, 1, 384), (384, 96)),
+                                    ((5, 13), (13, 7)), ((2, 3, 4, 33), (33, 5)), ((2, 8, 32), (2, 32, 96))])
+def test_matmul_bias(sess, as_, bs):
+    """TestMatMulBias (:326-368): fused bias on the packed path and the batched-rhs path; run 2 bit-identical."""
+    announce(f"op matmul bias {as_} {bs}")
+    rng = np.random.default_rng(9)
+    a = rng.uniform(-1, 1, as_).astype(np.float32)
+    b = rng.uniform(-1, 1, bs).astype(np.float32)
+    n = bs[-1]
+    bias = rng.uniform(-1, 1, n).astype(np.float32)
+    op = sess.op("MatMul", 1)
+    da, db, dbias = dev(sess, a), dev(sess, b), dev(sess, bias)
+    (y,) = run(op, da, db, dbias)
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64)) + bias
+    assert_close(y, want, nstar_tol(bs[-2], a, b) + 1e-6, "matmul bias")
+    (y2,) = run(op, da, db, dbias)
+    assert np.array_equal(y, y2), "second run differs"
+
+
+@pytest.mark.parametrize("as_,bs", [((128, 384), (384, 1536)), ((1, 16, 48), (48, 144)), ((2, 8, 32), (2, 32, 96))])
+def test_matmul_gelu(sess, as_, bs):
+    """TestMatMulGelu (:405-): ingot_act=gelu fused vs MatMul → ingot.Gelu."""
+    announce(f"op matmul gelu {as_} {bs}")
+    rng = np.random.default_rng(31)
+    a = rng.uniform(-1, 1, as_).astype(np.float32)
+    b = rng.uniform(-1, 1, bs).astype(np.float32)
+    bias = rng.uniform(-1, 1, bs[-1]).astype(np.float32)
+    da, db, dbias = dev(sess, a), dev(sess, b), dev(sess, bias)
+    (fused,) = run(sess.op("MatMul", 1, {"ingot_act": "gelu"}), da, db, dbias)
+    mm = sess.op("MatMul", 1).run(da, db, dbias)[0]
+    (sep,) = run(sess.op("Gelu", 1, domain="ingot"), mm)
+    mm.free()
+    assert_close(fused, sep, 1e-5, "fused vs separate gelu")
+    pre = np.matmul(a.astype(np.float64), b.astype(np.float64)) + bias
+    want = np.vectorize(lambda v: oracle.act(v, L.ACT_GELU_ERF))(pre)
+    assert_close(fused, want, nstar_tol(bs[-2], a, b) + 1e-6, "gelu vs oracle")
+
+
+@pytest.mark.parametrize("m,trans_b", [(37, 0), (37, 1), (1, 0), (1, 1), (3, 1), (16, 1), (17, 1)])
+def test_gemm_bf16_weight(sess, m, trans_b):
+    """TestGemmBF16Weight (ops/gemm_bf16_optest_test.go:29-63): K=300, N=29, alpha 0.5, beta 2."""
+    announce(f"op gemm bf16 m={m} transB={trans_b}")
+    rng = np.random.default_rng(81 + m + trans_b)
+    K, N = 300, 29
+    a = rng.uniform(-1, 1, (m, K)).astype(np.float32)
+    b = bf16_weights(rng, (N, K) if trans_b else (K, N))
+    c = rng.uniform(-1, 1, N).astype(np.float32)
+    op = sess.op("Gemm", 13, {"transB": trans_b, "alpha": 0.5, "beta": 2.0})
+    (y,) = run(op, dev(sess, a), dev(sess, b, L.DT_BF16), dev(sess, c))
+    want = oracle.gemm(a, b, trans_b=bool(trans_b), b_dtype=oracle.BF16, alpha=0.5, beta=2.0, c=c, c_mode=2)
+    assert_close(y, want, nstar_tol(K, a, oracle.bf16_to_f32(b)), "gemm bf16 weight")
+
+
+@pytest.mark.parametrize("cshape", [(6, 10), (10,), (1, 10), (6, 1), (1,), ()])
+def test_gemm_c_broadcast(sess, cshape):
+    announce(f"op gemm C {cshape}")
+    rng = np.random.default_rng(3)
+    a = rng.uniform(-1, 1, (6, 20)).astype(np.float32)
+    b = rng.uniform(-1, 1, (20, 10)).astype(np.float32)
+    c = rng.normal(size=cshape).astype(np.float32)
+    (y,) = run(sess.op("Gemm", 11, {"beta": 0.5}), dev(sess, a), dev(sess, b), dev(sess, c))
+    want = a.astype(np.float64) @ b.astype(np.float64) + 0.5 * np.broadcast_to(c.reshape(
+        cshape if len(cshape) == 2 else (-1,)), (6, 10))
+    assert_close(y, want, nstar_tol(20, a, b) + 1e-6, f"C {cshape}")
+
+
+def test_gemm_trans_a_and_errors(sess):
+    announce("op gemm transA")
+    rng = np.random.default_rng(4)
+    a = rng.uniform(-1, 1, (20, 6)).astype(np.float32)
+    b = rng.uniform(-1, 1, (10, 20)).astype(np.float32)
+    (y,) = run(sess.op("Gemm", 11, {"transA": 1, "transB": 1}), dev(sess, a), dev(sess, b))
+    assert_close(y, a.T.astype(np.float64) @ b.T.astype(np.float64), nstar_tol(20, a, b), "transA")
+    with pytest.raises(IngotError, match="inner dim mismatch"):
+        sess.op("Gemm", 11).run(dev(sess, a), dev(sess, b))
+    with pytest.raises(IngotError, match="cannot broadcast C"):
+        sess.op("Gemm", 11).run(dev(sess, a.T.copy()), dev(sess, b.T.copy()), dev(sess, np.zeros(7, np.float32)))
+    with pytest.raises(IngotError, match="need A and B"):
+        sess.op("Gemm", 11).run(dev(sess, a))
+
+
+def test_matmul_integer_op(sess):
+    """TestQLinearMatMulAndMatMulInteger's MatMulInteger half (ops/quant_optest_test.go:194-223)."""
+    announce("op matmulinteger")
+    k = KATS["matmul_integer"]
+    a = np.array(k["A"], np.uint8).reshape(k["m"], k["k"])
+    b = np.array(k["B"], np.int8).reshape(k["k"], k["n"])
+    op = sess.op("MatMulInteger", 10)
+    da, db = dev(sess, a, L.DT_U8), dev(sess, b, L.DT_I8)
+    (y,) = run(op, da, db, dev(sess, np.array([k["za"]], np.uint8), L.DT_U8), dev(sess, np.zeros(1, np.int8), L.DT_I8))
+    assert np.array_equal(y, np.array(k["Y"], np.int32))
+    with pytest.raises(IngotError, match="non-zero weight zero_point"):
+        op.run(da, db, None, dev(sess, np.array([1], np.int8), L.DT_I8))
+    with pytest.raises(IngotError, match="only s8 weights"):
+        op.run(da, dev(sess, b.view(np.uint8), L.DT_U8))
+
+
+def test_dequantize_linear_op(sess):
+    """TestDequantizeLinear (ops/quant_optest_test.go:60-73) + per-axis + axis errors."""
+    announce("op dequant")
+    op = sess.op("DequantizeLinear", 10)
+    (y,) = run(op, dev(sess, np.array([0, 128, 255], np.uint8), L.DT_U8), dev(sess, np.array([0.5], np.float32)),
+               dev(sess, np.array([128], np.uint8), L.DT_U8))
+    assert np.array_equal(y, np.array([-64, 0, 63.5], np.float32))
+    (y,) = run(op, dev(sess, np.array([-128, 127], np.int8), L.DT_I8), dev(sess, np.array([2.0], np.float32)),
+               dev(sess, np.array([-8], np.int8), L.DT_I8))
+    assert np.array_equal(y, np.array([-240, 270], np.float32))
+    rng = np.random.default_rng(2)
+    x = rng.integers(-1000, 1000, (4, 6, 3)).astype(np.int32)
+    sc = rng.uniform(0.01, 0.1, 6).astype(np.float32)
+    (y,) = run(op, dev(sess, x, L.DT_I32), dev(sess, sc))
+    assert np.array_equal(y, oracle.dequantize_linear(x, sc, inner=3))
+    with pytest.raises(IngotError, match="per-axis scale len"):
+        op.run(dev(sess, x, L.DT_I32), dev(sess, np.ones(5, np.float32)))
+
+
+@pytest.mark.parametrize("name,domain,attrs,code", [("Relu", "", {}, L.ACT_RELU), ("Gelu", "ingot", {}, L.ACT_GELU_ERF),
+                                                   ("Gelu", "", {"approximate": "tanh"}, L.ACT_GELU_TANH),
+                                                   ("Sigmoid", "", {}, L.ACT_SIGMOID)])
+def test_activation_nodes(sess, name, domain, attrs, code):
+    announce(f"op {name}")
+    rng = np.random.default_rng(8)
+    x = rng.normal(0, 3, (7, 33)).astype(np.float32)
+    (y,) = run(sess.op(name, 20 if domain == "" and name == "Gelu" else 13 if domain == "" else 1, attrs, domain),
+               dev(sess, x))
+    want = np.vectorize(lambda v: oracle.act(v, code))(x.astype(np.float64))
+    assert_close(y, want, 2e-6 * max(1.0, float(np.max(np.abs(want)))), name)
