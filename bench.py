@@ -87,7 +87,7 @@ class Dit:
 
     def step(self):
         for (k, n, _), w, y, act in zip(self.shapes, self.w, self.y, self.acts):
-            self.sess.gemm(self.a[k], w, y, self.M, act=act)
+            self.sess.gemm(self.a[k], w, y, self.M, act=act, math=self.L.MATH_BF16)
 
     def kernel_roofline(self):
         """The bf16 MFMA GEMM kernel alone: activations already bf16 (one launch per Gemm)."""

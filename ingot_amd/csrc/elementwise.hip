@@ -65,21 +65,28 @@ __global__ void colsum_kernel(const int8_t* packed, int64_t kp, int64_t n, int32
 }
 
 // Packs activations into [m][kl] rows of dst_kind, zero padded beyond k.
-// Each thread produces one 16-byte chunk of a destination row.
+// Each thread produces one 16-byte chunk of a destination row. KIND_BF16X2
+// writes two planes: hi = bf16(a) at dst, lo = bf16(a − hi) at dst + plane.
+__device__ __forceinline__ float load_a(const char* sb, int src_dt, int trans, int64_t lda, int64_t row, int64_t kk) {
+    const int64_t si = trans ? kk * lda + row : row * lda + kk;
+    return load_f(sb, src_dt, si);
+}
+
 template <int KD>
 __global__ void pack_a_kernel(const void* src, int src_dt, int64_t lda, int trans, int64_t m, int64_t k,
-                              int64_t src_stride, void* dst, int64_t kl, int64_t dst_stride) {
-    constexpr int EPC = KD == KIND_BF16 ? 8 : (KD == KIND_F32 ? 4 : 16);  // elements per chunk
+                              int64_t src_stride, void* dst, int64_t kl, int64_t dst_stride, int64_t plane) {
+    constexpr int EPC = KD == KIND_F32 ? 4 : (KD == KIND_I8 ? 16 : 8);  // elements per chunk
     const int64_t chunks_per_row = kl / EPC;
     const int64_t total = m * chunks_per_row;
     const int b = blockIdx.y;
     const char* sb = (const char*)src;
     const int esz = src_dt == INGOT_DT_F32 ? 4 : (src_dt == INGOT_DT_BF16 ? 2 : 1);
     sb += (int64_t)b * src_stride * esz;
+    const int esz_d = KD == KIND_F32 ? 4 : (KD == KIND_I8 ? 1 : 2);
     for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < total; c += (int64_t)gridDim.x * blockDim.x) {
         const int64_t row = c / chunks_per_row;
         const int64_t k0 = (c - row * chunks_per_row) * EPC;
-        i32x4_t out;
+        char* db = (char*)dst + ((int64_t)b * dst_stride + row * kl + k0) * esz_d;
         if (KD == KIND_I8) {
             uint8_t v[16];
 #pragma unroll
@@ -93,43 +100,45 @@ __global__ void pack_a_kernel(const void* src, int src_dt, int64_t lda, int tran
                 }
                 v[e] = x;
             }
+            i32x4_t out;
             __builtin_memcpy(&out, v, 16);
-        } else if (KD == KIND_BF16) {
-            uint16_t v[8];
+            *(i32x4_t*)db = out;
+        } else if (KD == KIND_F32) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = k0 + e < k ? load_a(sb, src_dt, trans, lda, row, k0 + e) : 0.f;
+            i32x4_t out;
+            __builtin_memcpy(&out, v, 16);
+            *(i32x4_t*)db = out;
+        } else {
+            float v[8];
             if (!trans && src_dt == INGOT_DT_F32 && k0 + 8 <= k && ((row * lda + k0) & 3) == 0 &&
                 (((uintptr_t)sb) & 15) == 0) {
                 const f32x4_t* s4 = (const f32x4_t*)((const float*)sb + row * lda + k0);
                 const f32x4_t lo = s4[0], hi = s4[1];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    v[e] = f32_to_bf16(lo[e]);
-                    v[e + 4] = f32_to_bf16(hi[e]);
+                    v[e] = lo[e];
+                    v[e + 4] = hi[e];
                 }
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int64_t kk = k0 + e;
-                    uint16_t x = 0;
-                    if (kk < k) {
-                        const int64_t si = trans ? kk * lda + row : row * lda + kk;
-                        x = src_dt == INGOT_DT_BF16 ? ((const uint16_t*)sb)[si] : f32_to_bf16(((const float*)sb)[si]);
-                    }
-                    v[e] = x;
-                }
+                for (int e = 0; e < 8; ++e) v[e] = k0 + e < k ? load_a(sb, src_dt, trans, lda, row, k0 + e) : 0.f;
             }
-            __builtin_memcpy(&out, v, 16);
-        } else {
-            float v[4];
+            uint16_t h[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int64_t kk = k0 + e;
-                v[e] = kk < k ? load_f(sb, src_dt, trans ? kk * lda + row : row * lda + kk) : 0.f;
+            for (int e = 0; e < 8; ++e) h[e] = f32_to_bf16(v[e]);
+            i32x4_t out;
+            __builtin_memcpy(&out, h, 16);
+            *(i32x4_t*)db = out;
+            if (KD == KIND_BF16X2) {
+                uint16_t l[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) l[e] = f32_to_bf16(v[e] - bf16_to_f32(h[e]));
+                __builtin_memcpy(&out, l, 16);
+                *(i32x4_t*)(db + plane * esz_d) = out;
             }
-            __builtin_memcpy(&out, v, 16);
         }
-        const int esz_d = KD == KIND_BF16 ? 2 : (KD == KIND_F32 ? 4 : 1);
-        char* db = (char*)dst + ((int64_t)b * dst_stride + row * kl + k0) * esz_d;
-        *(i32x4_t*)db = out;
     }
 }
 
@@ -182,20 +191,25 @@ hipError_t launch_colsum_i8(const int8_t* packed, int64_t kp, int64_t n, int32_t
 hipError_t launch_pack_a(const void* src, int src_dtype, int64_t lda, int trans, int64_t m, int64_t k,
                          int64_t src_stride, void* dst, GemmKind dst_kind, int64_t kl, int64_t dst_stride, int batch,
                          hipStream_t st) {
-    const int epc = dst_kind == KIND_BF16 ? 8 : (dst_kind == KIND_F32 ? 4 : 16);
+    const int epc = dst_kind == KIND_F32 ? 4 : (dst_kind == KIND_I8 ? 16 : 8);
     dim3 grid(grid_for(m * (kl / epc), 256), batch);
+    const int64_t plane = m * kl;
     switch (dst_kind) {
         case KIND_BF16:
             hipLaunchKernelGGL(pack_a_kernel<KIND_BF16>, grid, dim3(256), 0, st, src, src_dtype, lda, trans, m, k,
-                               src_stride, dst, kl, dst_stride);
+                               src_stride, dst, kl, dst_stride, plane);
+            break;
+        case KIND_BF16X2:
+            hipLaunchKernelGGL(pack_a_kernel<KIND_BF16X2>, grid, dim3(256), 0, st, src, src_dtype, lda, trans, m, k,
+                               src_stride, dst, kl, dst_stride, plane);
             break;
         case KIND_F32:
             hipLaunchKernelGGL(pack_a_kernel<KIND_F32>, grid, dim3(256), 0, st, src, src_dtype, lda, trans, m, k,
-                               src_stride, dst, kl, dst_stride);
+                               src_stride, dst, kl, dst_stride, plane);
             break;
         case KIND_I8:
             hipLaunchKernelGGL(pack_a_kernel<KIND_I8>, grid, dim3(256), 0, st, src, src_dtype, lda, trans, m, k,
-                               src_stride, dst, kl, dst_stride);
+                               src_stride, dst, kl, dst_stride, plane);
             break;
     }
     return hipGetLastError();

@@ -50,6 +50,11 @@ __device__ __forceinline__ void mma16<KIND_BF16>(f32x4_t& acc, const i32x4_t& x,
 }
 
 template <>
+__device__ __forceinline__ void mma16<KIND_BF16X2>(f32x4_t& acc, const i32x4_t& x, const i32x4_t& y) {
+    mma16<KIND_BF16>(acc, x, y);
+}
+
+template <>
 __device__ __forceinline__ void mma16<KIND_F32>(f32x4_t& acc, const i32x4_t& x, const i32x4_t& y) {
     const f32x4_t xf = __builtin_bit_cast(f32x4_t, x);
     const f32x4_t yf = __builtin_bit_cast(f32x4_t, y);
@@ -66,10 +71,12 @@ __device__ __forceinline__ void mma16<KIND_I8>(i32x4_t& acc, const i32x4_t& x, c
 
 template <int KD, int BM, int BN>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
+    constexpr bool SPLIT = KD == KIND_BF16X2;
+    constexpr int AP = SPLIT ? 2 : 1;  // activation planes
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TM = WM / 16, TN = WN / 16;
     constexpr int LA = BM / 32, LB = BN / 32;  // 16-byte chunks per thread per k-tile
-    constexpr int STAGE = (BM + BN) * PITCH;
+    constexpr int STAGE = (AP * BM + BN) * PITCH;
     static_assert(BM % 32 == 0 && BN % 32 == 0, "tile must be a multiple of 32");
     typedef typename AccOf<KD>::type Acc;
 
@@ -108,25 +115,29 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
         const int n = min(n0 + lrow + i * 32, p.b_rows - 1);
         pb[i] = p.b + (int64_t)n * p.ldb_bytes + lcol;
     }
-    i32x4_t ra[LA], rb[LB];
+    i32x4_t ra[AP][LA], rb[LB];
     const int axor = p.a_xor ? (int)0x80808080u : 0;
 
     auto gload = [&](int kt) {
         const int64_t off = (int64_t)kt * KTILE_BYTES;
 #pragma unroll
-        for (int i = 0; i < LA; ++i) ra[i] = *(const i32x4_t*)(pa[i] + off);
+        for (int pl = 0; pl < AP; ++pl)
+#pragma unroll
+            for (int i = 0; i < LA; ++i) ra[pl][i] = *(const i32x4_t*)(pa[i] + pl * p.a_plane_bytes + off);
 #pragma unroll
         for (int i = 0; i < LB; ++i) rb[i] = *(const i32x4_t*)(pb[i] + off);
     };
     auto lstore = [&](int buf) {
         char* sa = smem + buf * STAGE;
-        char* sb = sa + BM * PITCH;
+        char* sb = sa + AP * BM * PITCH;
 #pragma unroll
-        for (int i = 0; i < LA; ++i) {
-            i32x4_t v = ra[i];
-            if (KD == KIND_I8) v ^= axor;
-            *(i32x4_t*)(sa + (lrow + i * 32) * PITCH + lcol) = v;
-        }
+        for (int pl = 0; pl < AP; ++pl)
+#pragma unroll
+            for (int i = 0; i < LA; ++i) {
+                i32x4_t v = ra[pl][i];
+                if (KD == KIND_I8) v ^= axor;
+                *(i32x4_t*)(sa + (pl * BM + lrow + i * 32) * PITCH + lcol) = v;
+            }
 #pragma unroll
         for (int i = 0; i < LB; ++i) *(i32x4_t*)(sb + (lrow + i * 32) * PITCH + lcol) = rb[i];
     };
@@ -140,7 +151,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
     // fragment read offsets: lane row (lane % 16), 16-byte chunk (lane / 16)
     const int frag_off = (lane & 15) * PITCH + (lane >> 4) * 16;
     const int a_off = (wm * WM) * PITCH + frag_off;
-    const int b_off = BM * PITCH + (wn * WN) * PITCH + frag_off;
+    const int b_off = AP * BM * PITCH + (wn * WN) * PITCH + frag_off;
 
     gload(0);
     lstore(0);
@@ -153,15 +164,20 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
         const char* st = smem + cur * STAGE;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            i32x4_t fa[TM], fb[TN];
+            i32x4_t fa[AP][TM], fb[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) fa[i] = *(const i32x4_t*)(st + a_off + i * 16 * PITCH + s * 64);
+            for (int pl = 0; pl < AP; ++pl)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+                    fa[pl][i] = *(const i32x4_t*)(st + a_off + (pl * BM + i * 16) * PITCH + s * 64);
 #pragma unroll
             for (int j = 0; j < TN; ++j) fb[j] = *(const i32x4_t*)(st + b_off + j * 16 * PITCH + s * 64);
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+            for (int pl = 0; pl < AP; ++pl)
 #pragma unroll
-                for (int j = 0; j < TN; ++j) mma16<KD>(acc[i][j], fb[j], fa[i]);
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) mma16<KD>(acc[i][j], fb[j], fa[pl][i]);
         }
         if (more) lstore(cur ^ 1);
         __syncthreads();
@@ -248,6 +264,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
 // register footprint allow; eff: relative throughput per CU slot.
 const GemmConfig kBF16Cfgs[] = {{256, 192, 1, 1.00f}, {128, 128, 2, 0.80f}, {128, 64, 2, 0.65f}, {64, 64, 4, 0.45f}};
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 1.00f}, {128, 64, 2, 0.95f}, {64, 64, 4, 0.85f}};
+const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 1, 0.85f}, {64, 64, 2, 0.60f}};
 const GemmConfig kI8Cfgs[] = {{256, 192, 1, 1.00f}, {128, 128, 2, 0.80f}, {128, 64, 2, 0.65f}, {64, 64, 4, 0.45f}};
 
 template <int KD, int BM, int BN>
@@ -264,6 +281,7 @@ int gemm_configs(GemmKind kind, const GemmConfig** out) {
         case KIND_BF16: *out = kBF16Cfgs; return (int)(sizeof(kBF16Cfgs) / sizeof(kBF16Cfgs[0]));
         case KIND_F32: *out = kF32Cfgs; return (int)(sizeof(kF32Cfgs) / sizeof(kF32Cfgs[0]));
         case KIND_I8: *out = kI8Cfgs; return (int)(sizeof(kI8Cfgs) / sizeof(kI8Cfgs[0]));
+        case KIND_BF16X2: *out = kBF16X2Cfgs; return (int)(sizeof(kBF16X2Cfgs) / sizeof(kBF16X2Cfgs[0]));
     }
     return 0;
 }
@@ -283,6 +301,13 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 0: return launch_one<KIND_F32, 128, 128>(a, batch, st);
                 case 1: return launch_one<KIND_F32, 128, 64>(a, batch, st);
                 case 2: return launch_one<KIND_F32, 64, 64>(a, batch, st);
+            }
+            break;
+        case KIND_BF16X2:
+            switch (cfg) {
+                case 0: return launch_one<KIND_BF16X2, 128, 128>(a, batch, st);
+                case 1: return launch_one<KIND_BF16X2, 128, 64>(a, batch, st);
+                case 2: return launch_one<KIND_BF16X2, 64, 64>(a, batch, st);
             }
             break;
         case KIND_I8:

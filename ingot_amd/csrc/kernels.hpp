@@ -7,7 +7,11 @@
 namespace ingot {
 
 // Element kind of a packed GEMM operand pair (A and B share it).
-enum GemmKind { KIND_BF16 = 0, KIND_F32 = 1, KIND_I8 = 2 };
+// KIND_BF16X2: f32 activations carried as two bf16 planes (hi = bf16(a),
+// lo = bf16(a − hi)) against bf16 weights; two MFMAs per step keep the
+// activation error at ~2⁻¹⁷ relative (f32-class), where KIND_BF16 rounds
+// the activations once (~2⁻⁹).
+enum GemmKind { KIND_BF16 = 0, KIND_F32 = 1, KIND_I8 = 2, KIND_BF16X2 = 3 };
 
 // Every kernel row of A and B is read in 128-byte k-tiles: 64 bf16, 32 f32 or
 // 128 int8 elements. Packed operands are zero padded to whole k-tiles.
@@ -25,6 +29,7 @@ struct GemmArgs {
     int64_t stride_a_bytes;  // per blockIdx.y batch item
     int64_t stride_y;        // elements, per batch item
     int a_xor;               // int8: flip the sign bit of A bytes (u8 → s8)
+    int64_t a_plane_bytes;   // KIND_BF16X2: offset of the lo plane from the hi plane
     void* y;
     int64_t ldy;
     Epi epi;

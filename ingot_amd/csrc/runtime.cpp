@@ -40,8 +40,8 @@ int elem_size(int dt) {
 }
 
 // elements of a kind per 128-byte k-tile
-int ktile_elems(GemmKind k) { return k == KIND_BF16 ? 64 : (k == KIND_F32 ? 32 : 128); }
-int kind_size(GemmKind k) { return k == KIND_BF16 ? 2 : (k == KIND_F32 ? 4 : 1); }
+int ktile_elems(GemmKind k) { return k == KIND_F32 ? 32 : (k == KIND_I8 ? 128 : 64); }
+int kind_size(GemmKind k) { return k == KIND_F32 ? 4 : (k == KIND_I8 ? 1 : 2); }
 
 // Picks the tile configuration with the least estimated time: full rounds of
 // num_cus·occupancy workgroups, each round as long as the most loaded CU.
@@ -493,11 +493,16 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
         !getenv("INGOT_NO_GEMV"))
         return run_gemv(s, a);
 
-    const GemmKind kind = w->kind;
+    // bf16 weights with f32 activations: two bf16 planes (f32-class accuracy)
+    // unless the caller asked for single bf16 rounding (INGOT_MATH_BF16).
+    GemmKind kind = w->kind;
+    if (kind == KIND_BF16 && a->a_dtype == INGOT_DT_F32 && a->math != INGOT_MATH_BF16) kind = KIND_BF16X2;
     const int esz = kind_size(kind);
+    const int planes = kind == KIND_BF16X2 ? 2 : 1;
     const int64_t kl = round_up(a->K, ktile_elems(kind));
     const int a_esz = elem_size(a->a_dtype);
-    const bool a_native = (kind == KIND_BF16) == (a->a_dtype == INGOT_DT_BF16);
+    const bool a_native = (kind == KIND_BF16 && a->a_dtype == INGOT_DT_BF16) ||
+                          (kind == KIND_F32 && a->a_dtype == INGOT_DT_F32);
     const bool direct = a_native && !a->trans_a && a->K % ktile_elems(kind) == 0 && (a->lda * a_esz) % 16 == 0 &&
                         aligned16(a->d_a) && (batch == 1 || (a->stride_a * a_esz) % 16 == 0);
     GemmArgs g;
@@ -508,14 +513,16 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
         g.stride_a_bytes = a->stride_a * a_esz;
     } else {
         void* ws;
-        rc = ws_reserve(s, (size_t)(batch * a->M * kl * esz), &ws);
+        const int64_t plane = a->M * kl;
+        rc = ws_reserve(s, (size_t)(batch * planes * plane * esz), &ws);
         if (rc) return rc;
         hipError_t e = launch_pack_a(a->d_a, a->a_dtype, a->lda, a->trans_a, a->M, a->K, a->stride_a, ws, kind, kl,
-                                     a->M * kl, (int)batch, s->stream);
+                                     planes * plane, (int)batch, s->stream);
         if (e != hipSuccess) return hip_fail(e, "pack A");
         g.a = (const char*)ws;
         g.lda_bytes = kl * esz;
-        g.stride_a_bytes = a->M * kl * esz;
+        g.stride_a_bytes = planes * plane * esz;
+        g.a_plane_bytes = plane * esz;
     }
     g.b = (const char*)w->data;
     g.ldb_bytes = w->kp * esz;

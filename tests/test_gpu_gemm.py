@@ -50,6 +50,7 @@ def test_gemm_f32_weights(sess, m, n, k):
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
 def test_gemm_bf16_weights(sess, m, n, k):
+    """Default math for f32 A × bf16 W: activations as bf16 hi+lo planes (f32-class error)."""
     announce(f"gemm bf16 m={m} n={n} k={k}")
     rng = np.random.default_rng(m * 131 + n * 17 + k)
     a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
@@ -59,7 +60,26 @@ def test_gemm_bf16_weights(sess, m, n, k):
     got = run_gemm(sess, da, w, m)
     want = oracle.gemm(a, wb, trans_b=True, b_dtype=oracle.BF16)
     assert_close(got, want, nstar_tol(k, a, oracle.bf16_to_f32(wb)), f"bf16 {m}x{n}x{k}")
+    # the reference's bf16-weight op tolerance (ops/gemm_bf16_optest_test.go:57)
+    rel = np.max(np.abs(got - want) / (1 + np.abs(want)))
+    assert rel <= 1e-5 * math.sqrt(k), f"bf16x2 relative error {rel:.3e}"
     w.free(), da.free()
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_gemm_bf16_math_rounds_activations(sess, m, n, k):
+    """INGOT_MATH_BF16 (GPUBF16 semantics): A rounded to bf16 once; exact up to f32 accumulation."""
+    announce(f"gemm bf16-math m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 7 + n * 5 + k)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k))
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    got = run_gemm(sess, sess.to_device(a), w, m, math=L.MATH_BF16)
+    a16 = oracle.bf16_to_f32(oracle.f32_to_bf16(a))
+    want = oracle.gemm(a16, wb, trans_b=True, b_dtype=oracle.BF16)
+    rel = np.max(np.abs(got - want) / (1 + np.abs(want)))
+    assert rel <= 1e-5 * math.sqrt(k), f"bf16 math relative error {rel:.3e}"
+    w.free()
 
 
 @pytest.mark.parametrize("mode", [L.C_FULL, L.C_ROW, L.C_COL, L.C_SCALAR])
@@ -209,18 +229,22 @@ def test_config2_bert_f32(sess, k, n, act):
 
 @pytest.mark.parametrize("k,n,act", [(3072, 9216, 0), (3072, 12288, L.ACT_GELU_ERF), (12288, 3072, 0)])
 def test_config5_dit_bf16(sess, k, n, act):
-    """DiT GEMMs, M=4096, A f32 → bf16 RNE on load, W bf16 [N,K], f32 accumulate."""
+    """DiT GEMMs, M=4096, A f32 → bf16 RNE on load (INGOT_MATH_BF16, the benched path),
+    W bf16 [N,K], f32 accumulate; north-star bound against the f32-A oracle."""
     announce(f"dit k={k} n={n}")
     rng = np.random.default_rng(k * 3 + n)
     a = rng.normal(0, 1, (4096, k)).astype(np.float32)
     wb = bf16_weights(rng, (n, k), 0.02, "normal")
     w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
     da = sess.to_device(a)
-    got = run_gemm(sess, da, w, 4096, act=act)
+    got = run_gemm(sess, da, w, 4096, act=act, math=L.MATH_BF16)
     rows = np.arange(5, 4096, 257)
     want = oracle.gemm(a[rows], wb, trans_b=True, b_dtype=oracle.BF16, act_code=act)
     assert_close(got[rows], want, nstar_tol(k, a, oracle.bf16_to_f32(wb)), f"dit {k}x{n}")
-    assert np.array_equal(run_gemm(sess, da, w, 4096, act=act), got), "run-to-run bit identity"
+    assert np.array_equal(run_gemm(sess, da, w, 4096, act=act, math=L.MATH_BF16), got), "run-to-run bit identity"
+    # default math (bf16 hi+lo activations) on the same inputs
+    got2 = run_gemm(sess, da, w, 4096, act=act)
+    assert_close(got2[rows], want, 1e-5 * math.sqrt(k) * (1 + np.abs(want).max()), f"dit x2 {k}x{n}")
     w.free(), da.free()
 
 
