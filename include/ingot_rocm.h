@@ -168,9 +168,12 @@ int ingot_rocm_weight_info(const ingot_rocm_weight* w, int64_t* n, int64_t* k, i
  * (kernels/metal/gemmep.go:68). B is a packed weight (logical [N,K]).
  *   a_dtype : INGOT_DT_F32 or INGOT_DT_BF16 (bf16-resident activations).
  *   trans_a : A is stored [K,M] (Gemm transA=1).
- *   math    : INGOT_MATH_AUTO follows the weight's packed dtype; f32 A with
- *             bf16 weights is rounded to bf16 (RNE) on its way in; the
- *             accumulation is always f32.
+ *   math    : INGOT_MATH_AUTO follows the weight's packed dtype. f32 A with
+ *             bf16 weights then runs as two bf16 planes (hi = bf16(a),
+ *             lo = bf16(a − hi)), keeping the reference's f32-activation
+ *             accuracy (~2⁻¹⁷ relative). INGOT_MATH_BF16 rounds A to bf16
+ *             once (RNE), the GPUBF16 semantics of graph/device.go:20-30, at
+ *             half the MFMA work. The accumulation is always f32.
  *   C       : d_c with c_mode INGOT_C_* and ldc (INGOT_C_FULL only).
  * M <= 16 with bf16 weights runs the split-K GEMV kernel. */
 typedef struct ingot_rocm_gemm_args {

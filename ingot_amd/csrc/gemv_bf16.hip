@@ -9,7 +9,8 @@
 // split into bf16 hi + lo parts (hi = bf16(x), lo = bf16(x − hi); |x − hi −
 // lo| <= 2⁻¹⁷|x|) and both are multiplied: bf16×bf16 products are exact in
 // f32, so the only roundings are the f32 accumulations, as in the reference's
-// f32 dot (kernels/vek/vek_generic.go:183-190).
+// f32 dot (kernels/vek/vek_generic.go:183-190). Under INGOT_MATH_BF16
+// (split = 0) only the hi part is used: x rounded to bf16 once.
 //
 // Work split: a workgroup (4 waves) owns 64 weight rows and one K slice of
 // KS elements; the grid's y dimension splits K (wavefront split-K). Lane
@@ -61,7 +62,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvArgs p) {
         const float v = k < p.K ? p.x[(int64_t)m * p.ldx + k] : 0.f;
         const uint16_t h = f32_to_bf16(v);
         xhi[m * XP + kk] = h;
-        xlo[m * XP + kk] = f32_to_bf16(v - bf16_to_f32(h));
+        xlo[m * XP + kk] = p.split ? f32_to_bf16(v - bf16_to_f32(h)) : (uint16_t)0;
     }
     __syncthreads();
 
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvArgs p) {
             const i32x4_t l = xrow ? *(const i32x4_t*)(xl + t * KR + u * 8) : zero;
             const bf16x8_t wv = __builtin_bit_cast(bf16x8_t, w[u]);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, h), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, l), acc, 0, 0, 0);
+            if (p.split) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, l), acc, 0, 0, 0);
         }
         if (more) {
 #pragma unroll

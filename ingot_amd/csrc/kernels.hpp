@@ -54,6 +54,7 @@ struct GemvArgs {
     int64_t ldw;
     int N;
     int S;               // k splits
+    int split;           // 1: x as bf16 hi + lo (f32-class); 0: x rounded to bf16 once
     int KS;              // k per split (multiple of 256)
     float* part;         // S > 1: partial sums [ceil(N/64)][S][M][64]
     unsigned* cnt;       // S > 1: zeroed arrival counters, one per 64-row block

@@ -433,6 +433,7 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     g.ldw = w->kp;
     g.N = (int)a->N;
     g.S = (int)S;
+    g.split = a->math == INGOT_MATH_BF16 ? 0 : 1;
     g.KS = (int)(w->kp / S);
     g.part = nullptr;
     g.cnt = s->counters;
