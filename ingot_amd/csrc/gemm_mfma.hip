@@ -5,22 +5,25 @@
 //   bf16: v_mfma_f32_16x16x32_bf16 (8 bf16 per lane)
 //   f32 : 4 × v_mfma_f32_16x16x4_f32 (one float per lane each)
 //   int8: v_mfma_i32_16x16x64_i8 (16 int8 per lane)
-// so one LDS layout (rows of 128-byte k-tiles, 16-byte pad to keep the
-// 16-lane ds_read_b128 phases conflict free) and one k-slot mapping serve
-// all three. Within an MFMA, lane group g = lane/16 supplies the 16-byte
-// chunk g of the current 64-byte half of the k-tile for both operands, so
-// the reduction pairs the same k on both sides.
+// so one LDS layout and one k-slot mapping serve all three. LDS rows are the
+// 128-byte k-tiles of A and B rows, unpadded, with 16-byte chunk c of row r
+// stored at position c ^ swz(r), which spreads the 16 rows a ds_read_b128
+// phase reads over distinct banks. Within an MFMA, lane group g = lane/16 supplies chunk g of
+// the current 64-byte half of the k-tile for both operands, so the reduction
+// pairs the same k on both sides.
 //
 // The weight is the first MFMA operand (rows n) and A the second (rows m):
-// D[n][m] lands in lane (m%16, n/4) as 4 consecutive n, stored as one float4
-// (or int4) per lane.
+// D[n][m] lands in lane (m%16, n/4) as 4 consecutive n.
 //
 // Workgroup: 256 threads = 4 waves in a 2×2 grid, each wave a
-// (BM/2)×(BN/2) sub-tile of 16×16 MFMA blocks. A and B k-tiles are staged
-// global → registers → LDS with two LDS buffers (one barrier per k-tile);
-// the next k-tile's global loads are in flight while the current one is
-// multiplied. Tile order is XCD-aware (consecutive tiles of the grouped
-// order run on one XCD's L2) and grouped by GROUP_M tile rows.
+// (BM/2)×(BN/2) sub-tile of 16×16 MFMA blocks, accumulators in AGPRs. A and B
+// k-tiles move global → LDS by DMA (buffer_load_dwordx4 ... lds): no staging
+// registers, 32-bit buffer offsets, hardware zero-fill past the operand end.
+// Two LDS stages: the next k-tile's DMA is in flight while the current one is
+// multiplied, one barrier per k-tile. Tile order is XCD-aware (consecutive
+// tiles of the grouped order run on one XCD's L2) and grouped by GROUP_M tile
+// rows. The epilogue (bias/C, activation, post scale/shift, or the int8
+// column-sum correction + dequant) runs on the staged accumulators.
 //
 // Reference counterparts: the packed-B sweep + micro-kernel of
 // kernels/gemm/gemm.go:280-334,431-490 (f32), PackBBF16/widenPanel
@@ -34,7 +37,6 @@ namespace ingot {
 
 namespace {
 
-constexpr int PITCH = KTILE_BYTES + 16;  // LDS row pitch in bytes
 constexpr int GROUP_M = 4;
 
 template <int KD> struct AccOf { typedef f32x4_t type; };
@@ -69,23 +71,48 @@ __device__ __forceinline__ void mma16<KIND_I8>(i32x4_t& acc, const i32x4_t& x, c
     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x, y, acc, 0, 0, 0);
 }
 
-template <int KD, int BM, int BN>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+#define LDS_AS(ptr) ((__attribute__((address_space(3))) void*)(ptr))
+
+// The workgroup barrier does not wait for LDS-DMA loads (they count as
+// vector-memory loads, not LDS stores), so every wave drains its own DMA and
+// LDS traffic first: s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(0).
+__device__ __forceinline__ void dma_barrier() {
+    __builtin_amdgcn_s_waitcnt(0x0070);
+    __syncthreads();
+}
+
+// LDS chunk swizzle: 16-byte chunk c of tile row r is stored at position
+// c ^ swz(r). (r >> 1) & 7 makes the 16 rows a ds_read_b128 phase touches
+// land on 16 distinct 16-byte bank groups of a 256-byte bank line.
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+
+template <int KD, int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     constexpr bool SPLIT = KD == KIND_BF16X2;
     constexpr int AP = SPLIT ? 2 : 1;  // activation planes
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int NW = WGM * WGN;      // waves per workgroup
+    constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 16, TN = WN / 16;
-    constexpr int LA = BM / 32, LB = BN / 32;  // 16-byte chunks per thread per k-tile
-    constexpr int STAGE = (AP * BM + BN) * PITCH;
+    constexpr int IA = BM / (8 * NW), IB = BN / (8 * NW);  // 8-row DMA loads per wave per k-tile (A plane, B)
+    static_assert(IA * 8 * NW == BM && IB * 8 * NW == BN, "DMA rows must split evenly over the waves");
+    constexpr int STAGE = (AP * BM + BN) * KTILE_BYTES;
     static_assert(BM % 32 == 0 && BN % 32 == 0, "tile must be a multiple of 32");
     typedef typename AccOf<KD>::type Acc;
 
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    // Two LDS stages, separate objects so the compiler can tell a stage being
+    // filled by DMA from the one being read. Rows are 128 bytes, unpadded; the
+    // 16-byte chunk c of row r sits at position c ^ (r % 8).
+    __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int wm = wave / WGN, wn = wave % WGN;
 
     // ---- tile coordinates: XCD-contiguous, then grouped along M ----
     const int nt = p.tiles_m * p.tiles_n;
@@ -99,47 +126,41 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
     const int m0 = (first_m + in_grp % gsz) * BM;
     const int n0 = (in_grp / gsz) * BN;
 
-    // ---- global load addressing (rows clamped; garbage rows are never stored) ----
-    const char* A = p.a + (int64_t)blockIdx.y * p.stride_a_bytes;
-    const int lrow = tid >> 3;
-    const int lcol = (tid & 7) * 16;
-    const char* pa[LA];
-    const char* pb[LB];
+    // ---- global → LDS DMA (buffer_load_dwordx4 ... lds) ----
+    // One instruction moves 8 rows × 128 bytes: lane l fetches row l/8, global
+    // chunk (l%8) ^ (l/8), landing at LDS position l%8 of that row. Loads past
+    // a buffer's end return zero (rows >= M; the weight is padded anyway).
+    const __amdgpu_buffer_rsrc_t rsa = make_rsrc(p.a + (int64_t)blockIdx.y * p.stride_a_bytes, p.a_bytes);
+    const __amdgpu_buffer_rsrc_t rsb = make_rsrc(p.b, p.b_bytes);
+    // Lane l of a DMA covering rows R..R+7 (R a multiple of 8) writes position
+    // l%8 of row R + l/8, so it fetches chunk (l%8) ^ swz(R + l/8); swz depends
+    // on R only through bit 3 of R, giving two offsets per lane.
+    const int lr = lane >> 3, lp = lane & 7;
+    uint32_t voff_a[2], voff_b[2];
 #pragma unroll
-    for (int i = 0; i < LA; ++i) {
-        const int m = min(m0 + lrow + i * 32, p.M - 1);
-        pa[i] = A + (int64_t)m * p.lda_bytes + lcol;
+    for (int h = 0; h < 2; ++h) {
+        const int c = lp ^ swz(h * 8 + lr);
+        voff_a[h] = (uint32_t)(lr * p.lda_bytes) + (uint32_t)(c << 4);
+        voff_b[h] = (uint32_t)(lr * p.ldb_bytes) + (uint32_t)(c << 4);
     }
-#pragma unroll
-    for (int i = 0; i < LB; ++i) {
-        const int n = min(n0 + lrow + i * 32, p.b_rows - 1);
-        pb[i] = p.b + (int64_t)n * p.ldb_bytes + lcol;
-    }
-    i32x4_t ra[AP][LA], rb[LB];
-    const int axor = p.a_xor ? (int)0x80808080u : 0;
 
-    auto gload = [&](int kt) {
-        const int64_t off = (int64_t)kt * KTILE_BYTES;
+    auto dma = [&](char* st, int kt) {
+        const uint32_t kofs = (uint32_t)kt * KTILE_BYTES;
 #pragma unroll
         for (int pl = 0; pl < AP; ++pl)
 #pragma unroll
-            for (int i = 0; i < LA; ++i) ra[pl][i] = *(const i32x4_t*)(pa[i] + pl * p.a_plane_bytes + off);
-#pragma unroll
-        for (int i = 0; i < LB; ++i) rb[i] = *(const i32x4_t*)(pb[i] + off);
-    };
-    auto lstore = [&](int buf) {
-        char* sa = smem + buf * STAGE;
-        char* sb = sa + AP * BM * PITCH;
-#pragma unroll
-        for (int pl = 0; pl < AP; ++pl)
-#pragma unroll
-            for (int i = 0; i < LA; ++i) {
-                i32x4_t v = ra[pl][i];
-                if (KD == KIND_I8) v ^= axor;
-                *(i32x4_t*)(sa + (pl * BM + lrow + i * 32) * PITCH + lcol) = v;
+            for (int j = 0; j < IA; ++j) {
+                const int r = (j * NW + wave) * 8;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rsa, LDS_AS(st + (pl * BM + r) * KTILE_BYTES), 16, voff_a[(r >> 3) & 1],
+                    (uint32_t)((m0 + r) * p.lda_bytes + pl * p.a_plane_bytes) + kofs, 0, 0);
             }
 #pragma unroll
-        for (int i = 0; i < LB; ++i) *(i32x4_t*)(sb + (lrow + i * 32) * PITCH + lcol) = rb[i];
+        for (int j = 0; j < IB; ++j) {
+            const int r = (j * NW + wave) * 8;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, LDS_AS(st + (AP * BM + r) * KTILE_BYTES), 16, voff_b[(r >> 3) & 1],
+                                                     (uint32_t)((n0 + r) * p.ldb_bytes) + kofs, 0, 0);
+        }
     };
 
     Acc acc[TM][TN];
@@ -148,51 +169,74 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = Acc{0, 0, 0, 0};
 
-    // fragment read offsets: lane row (lane % 16), 16-byte chunk (lane / 16)
-    const int frag_off = (lane & 15) * PITCH + (lane >> 4) * 16;
-    const int a_off = (wm * WM) * PITCH + frag_off;
-    const int b_off = AP * BM * PITCH + (wn * WN) * PITCH + frag_off;
+    // fragment offsets: lane row fr = lane % 16, chunk (s·4 + lane/16) of the k-tile
+    const int fr = lane & 15, fg = lane >> 4;
+    int a_off[2], b_off[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int pos = ((s * 4 + fg) ^ swz(fr)) << 4;
+        a_off[s] = (wm * WM + fr) * KTILE_BYTES + pos;
+        b_off[s] = (AP * BM + wn * WN + fr) * KTILE_BYTES + pos;
+    }
+    const int axor = p.a_xor ? (int)0x80808080u : 0;
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
+    typedef i32x4_t FragA[AP][TM];
+    typedef i32x4_t FragB[TN];
+    auto read_frags = [&](const char* st, int s, FragA& fa, FragB& fb) {
+#pragma unroll
+        for (int pl = 0; pl < AP; ++pl)
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                fa[pl][i] = *(const i32x4_t*)(st + a_off[s] + (pl * BM + i * 16) * KTILE_BYTES);
+                if (KD == KIND_I8) fa[pl][i] ^= axor;
+            }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[j] = *(const i32x4_t*)(st + b_off[s] + j * 16 * KTILE_BYTES);
+    };
+    auto mma_all = [&](const FragA& fa, const FragB& fb) {
+#pragma unroll
+        for (int pl = 0; pl < AP; ++pl)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) mma16<KD>(acc[i][j], fb[j], fa[pl][i]);
+    };
 
+    // Software pipeline over k-tiles, two LDS stages and two fragment sets.
+    // The k-tile's second-half fragments are read while its first half is
+    // multiplied; the barrier sits between the halves (all reads of the
+    // stage are done, the next stage's DMA has landed); right after it the
+    // stage just consumed is refilled two k-tiles ahead and the next
+    // k-tile's first-half fragments are read while the second half is
+    // multiplied.
+    FragA fa0, fa1;
+    FragB fb0, fb1;
+    dma(lds0, 0);
+    if (p.kt > 1) dma(lds1, 1);
+    dma_barrier();  // k-tile 0 (and 1) in LDS
+    read_frags(lds0, 0, fa0, fb0);
     for (int kt = 0; kt < p.kt; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < p.kt;
-        if (more) gload(kt + 1);
-        const char* st = smem + cur * STAGE;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            i32x4_t fa[AP][TM], fb[TN];
-#pragma unroll
-            for (int pl = 0; pl < AP; ++pl)
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-                    fa[pl][i] = *(const i32x4_t*)(st + a_off + (pl * BM + i * 16) * PITCH + s * 64);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) fb[j] = *(const i32x4_t*)(st + b_off + j * 16 * PITCH + s * 64);
-#pragma unroll
-            for (int pl = 0; pl < AP; ++pl)
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j) mma16<KD>(acc[i][j], fb[j], fa[pl][i]);
-        }
-        if (more) lstore(cur ^ 1);
-        __syncthreads();
+        char* cur = (kt & 1) ? lds1 : lds0;
+        char* nxt = (kt & 1) ? lds0 : lds1;
+        read_frags(cur, 1, fa1, fb1);
+        mma_all(fa0, fb0);
+        dma_barrier();  // cur fully read by every wave; k-tile kt+1 landed in nxt
+        if (kt + 2 < p.kt) dma(cur, kt + 2);
+        if (kt + 1 < p.kt) read_frags(nxt, 0, fa0, fb0);
+        mma_all(fa1, fb1);
     }
 
     // ---- epilogue ----
-    // Each wave stages half of its sub-tile at a time through its own LDS
-    // region (the k-loop's buffers are free now): lanes write their 4-wide
-    // column strips, then the wave walks the staged rows with row-contiguous
-    // 16-byte stores. Accumulators are only indexed statically.
-    constexpr int HR = WM / 2;          // rows per pass
-    constexpr int SP = WN + 4;          // staging pitch (elements)
-    static_assert(4 * HR * SP * 4 <= 2 * STAGE, "staging must fit in LDS");
+    // Each wave stages a slice of its sub-tile at a time through its own part
+    // of lds0: lanes write their 4-wide column strips, then the wave walks the
+    // staged rows with row-contiguous 16-byte stores. Accumulators are only
+    // indexed statically.
+    constexpr int SP = WN + 4;  // staging pitch (elements)
+    constexpr int NP = (NW * (WM / 2) * SP * 4 <= STAGE) ? 2 : ((NW * (WM / 4) * SP * 4 <= STAGE) ? 4 : 8);
+    constexpr int HR = WM / NP;  // rows per pass
+    static_assert(TM % NP == 0 && NW * HR * SP * 4 <= STAGE, "staging must fit in one LDS stage");
     static_assert(WN % 4 == 0, "row width must be whole float4s");
-    char* stage = smem + wave * (HR * SP * 4);
+    char* stage = lds0 + wave * (HR * SP * 4);
     const int r = lane & 15;
     const int g4 = (lane >> 4) * 4;
     const int row0 = m0 + wm * WM;
@@ -206,12 +250,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
         ybase = (uintptr_t)((float*)p.y + ybatch);
     const bool vec_ok = (ybase & 15) == 0 && (p.ldy & 3) == 0;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < NP; ++h) {
 #pragma unroll
-        for (int i = 0; i < TM / 2; ++i)
+        for (int i = 0; i < TM / NP; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j)
-                *(Acc*)(stage + ((i * 16 + r) * SP + j * 16 + g4) * 4) = acc[h * (TM / 2) + i][j];
+                *(Acc*)(stage + ((i * 16 + r) * SP + j * 16 + g4) * 4) = acc[h * (TM / NP) + i][j];
         __syncthreads();
         constexpr int Q = WN / 4;  // float4 per staged row
         for (int idx = lane; idx < HR * Q; idx += 64) {
@@ -261,16 +305,18 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p) {
 }
 
 // Tile configurations per kind. occupancy: workgroups per CU the LDS and
-// register footprint allow; eff: relative throughput per CU slot.
-const GemmConfig kBF16Cfgs[] = {{256, 192, 1, 1.00f}, {128, 128, 2, 0.80f}, {128, 64, 2, 0.65f}, {64, 64, 4, 0.45f}};
+// register footprint allow; eff: relative throughput per CU slot (measured
+// on MI355X for the bf16 kernel).
+const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.80f}, {128, 128, 2, 0.90f}, {128, 64, 2, 0.85f},
+                                {64, 64, 4, 0.45f}};
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 1.00f}, {128, 64, 2, 0.95f}, {64, 64, 4, 0.85f}};
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 1, 0.85f}, {64, 64, 2, 0.60f}};
-const GemmConfig kI8Cfgs[] = {{256, 192, 1, 1.00f}, {128, 128, 2, 0.80f}, {128, 64, 2, 0.65f}, {64, 64, 4, 0.45f}};
+const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.90f}, {128, 64, 2, 0.85f}, {64, 64, 4, 0.45f}};
 
-template <int KD, int BM, int BN>
+template <int KD, int BM, int BN, int WGM, int WGN>
 hipError_t launch_one(const GemmArgs& a, int batch, hipStream_t st) {
     dim3 grid(a.tiles_m * a.tiles_n, batch);
-    hipLaunchKernelGGL((gemm_kernel<KD, BM, BN>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_kernel<KD, BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), 0, st, a);
     return hipGetLastError();
 }
 
@@ -290,32 +336,33 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
     switch (kind) {
         case KIND_BF16:
             switch (cfg) {
-                case 0: return launch_one<KIND_BF16, 256, 192>(a, batch, st);
-                case 1: return launch_one<KIND_BF16, 128, 128>(a, batch, st);
-                case 2: return launch_one<KIND_BF16, 128, 64>(a, batch, st);
-                case 3: return launch_one<KIND_BF16, 64, 64>(a, batch, st);
-            }
-            break;
-        case KIND_F32:
-            switch (cfg) {
-                case 0: return launch_one<KIND_F32, 128, 128>(a, batch, st);
-                case 1: return launch_one<KIND_F32, 128, 64>(a, batch, st);
-                case 2: return launch_one<KIND_F32, 64, 64>(a, batch, st);
+                case 0: return launch_one<KIND_BF16, 256, 256, 2, 4>(a, batch, st);
+                case 1: return launch_one<KIND_BF16, 256, 192, 2, 2>(a, batch, st);
+                case 2: return launch_one<KIND_BF16, 128, 128, 2, 2>(a, batch, st);
+                case 3: return launch_one<KIND_BF16, 128, 64, 2, 2>(a, batch, st);
+                case 4: return launch_one<KIND_BF16, 64, 64, 2, 2>(a, batch, st);
             }
             break;
         case KIND_BF16X2:
             switch (cfg) {
-                case 0: return launch_one<KIND_BF16X2, 128, 128>(a, batch, st);
-                case 1: return launch_one<KIND_BF16X2, 128, 64>(a, batch, st);
-                case 2: return launch_one<KIND_BF16X2, 64, 64>(a, batch, st);
+                case 0: return launch_one<KIND_BF16X2, 128, 128, 2, 2>(a, batch, st);
+                case 1: return launch_one<KIND_BF16X2, 128, 64, 2, 2>(a, batch, st);
+                case 2: return launch_one<KIND_BF16X2, 64, 64, 2, 2>(a, batch, st);
+            }
+            break;
+        case KIND_F32:
+            switch (cfg) {
+                case 0: return launch_one<KIND_F32, 128, 128, 2, 2>(a, batch, st);
+                case 1: return launch_one<KIND_F32, 128, 64, 2, 2>(a, batch, st);
+                case 2: return launch_one<KIND_F32, 64, 64, 2, 2>(a, batch, st);
             }
             break;
         case KIND_I8:
             switch (cfg) {
-                case 0: return launch_one<KIND_I8, 256, 192>(a, batch, st);
-                case 1: return launch_one<KIND_I8, 128, 128>(a, batch, st);
-                case 2: return launch_one<KIND_I8, 128, 64>(a, batch, st);
-                case 3: return launch_one<KIND_I8, 64, 64>(a, batch, st);
+                case 0: return launch_one<KIND_I8, 256, 256, 2, 4>(a, batch, st);
+                case 1: return launch_one<KIND_I8, 128, 128, 2, 2>(a, batch, st);
+                case 2: return launch_one<KIND_I8, 128, 64, 2, 2>(a, batch, st);
+                case 3: return launch_one<KIND_I8, 64, 64, 2, 2>(a, batch, st);
             }
             break;
     }

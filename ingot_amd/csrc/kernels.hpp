@@ -30,6 +30,8 @@ struct GemmArgs {
     int64_t stride_y;        // elements, per batch item
     int a_xor;               // int8: flip the sign bit of A bytes (u8 → s8)
     int64_t a_plane_bytes;   // KIND_BF16X2: offset of the lo plane from the hi plane
+    uint32_t a_bytes;        // extent of one batch item's A (all planes): loads past it return 0
+    uint32_t b_bytes;        // extent of the packed weight
     void* y;
     int64_t ldy;
     Epi epi;

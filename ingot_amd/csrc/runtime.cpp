@@ -508,6 +508,13 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
                         aligned16(a->d_a) && (batch == 1 || (a->stride_a * a_esz) % 16 == 0);
     GemmArgs g;
     memset(&g, 0, sizeof g);
+    // Every GEMM operand is addressed with 32-bit buffer offsets.
+    const int64_t b_extent = w->np * w->kp * esz;
+    const int64_t a_extent = direct ? (a->M - 1) * a->lda * a_esz + kl * esz : (int64_t)planes * a->M * kl * esz;
+    if (b_extent >= ((int64_t)1 << 31) || a_extent >= ((int64_t)1 << 31))
+        return fail(INGOT_EDECLINED, "gemm: operand larger than 2 GiB");
+    g.a_bytes = (uint32_t)a_extent;
+    g.b_bytes = (uint32_t)b_extent;
     if (direct) {
         g.a = (const char*)a->d_a;
         g.lda_bytes = a->lda * a_esz;
@@ -567,6 +574,11 @@ int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64
     const bool direct = K % 128 == 0 && lda % 16 == 0 && aligned16(d_a);
     GemmArgs g;
     memset(&g, 0, sizeof g);
+    const int64_t a_extent = direct ? (M - 1) * lda + kl : M * kl;
+    if (w->np * w->kp >= ((int64_t)1 << 31) || a_extent >= ((int64_t)1 << 31))
+        return fail(INGOT_EDECLINED, "matmul_integer: operand larger than 2 GiB");
+    g.a_bytes = (uint32_t)a_extent;
+    g.b_bytes = (uint32_t)(w->np * w->kp);
     if (direct) {
         g.a = (const char*)d_a;
         g.lda_bytes = lda;
