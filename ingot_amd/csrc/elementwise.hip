@@ -34,10 +34,11 @@ inline unsigned grid_for(int64_t work, int per_block) {
 // dst[j][k] (np × kp, dst_kind) = src element (j, k) of the logical [n][k]
 // weight, zero outside n × k. One thread per destination element.
 __global__ void pack_weight_kernel(const void* src, int src_dt, int64_t ld, int trans, int64_t n, int64_t k,
-                                   void* dst, int dst_kind, int64_t np, int64_t kp) {
+                                   void* dst, int dst_kind, int64_t np, int64_t kp, int64_t ldk) {
     const int64_t total = np * kp;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t j = i / kp, kk = i - j * kp;
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t j = t / kp, kk = t - j * kp;
+        const int64_t i = j * ldk + kk;
         const bool in = j < n && kk < k;
         const int64_t si = trans ? j * ld + kk : kk * ld + j;
         if (dst_kind == KIND_I8) {
@@ -54,12 +55,12 @@ __global__ void pack_weight_kernel(const void* src, int src_dt, int64_t ld, int 
 }
 
 // One wave per row: colsum[j] = Σ_k packed[j][k] (int32 wrap-around).
-__global__ void colsum_kernel(const int8_t* packed, int64_t kp, int64_t n, int32_t* colsum) {
+__global__ void colsum_kernel(const int8_t* packed, int64_t kp, int64_t ldk, int64_t n, int32_t* colsum) {
     const int64_t j = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (j >= n) return;
     uint32_t s = 0;
-    for (int64_t k = lane; k < kp; k += 64) s += (uint32_t)(int32_t)packed[j * kp + k];
+    for (int64_t k = lane; k < kp; k += 64) s += (uint32_t)(int32_t)packed[j * ldk + k];
     for (int off = 32; off > 0; off >>= 1) s += (uint32_t)__shfl_xor((int)s, off);
     if (lane == 0) colsum[j] = (int32_t)s;
 }
@@ -177,14 +178,15 @@ __global__ void fill_kernel(uint8_t* d, uint8_t v, size_t bytes) {
 }  // namespace
 
 hipError_t launch_pack_weight(const void* src, int src_dtype, int64_t ld, int trans, int64_t n, int64_t k, void* dst,
-                              GemmKind dst_kind, int64_t np, int64_t kp, hipStream_t st) {
+                              GemmKind dst_kind, int64_t np, int64_t kp, int64_t ldk, hipStream_t st) {
     hipLaunchKernelGGL(pack_weight_kernel, dim3(grid_for(np * kp, 256)), dim3(256), 0, st, src, src_dtype, ld, trans, n,
-                       k, dst, (int)dst_kind, np, kp);
+                       k, dst, (int)dst_kind, np, kp, ldk);
     return hipGetLastError();
 }
 
-hipError_t launch_colsum_i8(const int8_t* packed, int64_t kp, int64_t n, int32_t* colsum, hipStream_t st) {
-    hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, packed, kp, n, colsum);
+hipError_t launch_colsum_i8(const int8_t* packed, int64_t kp, int64_t ldk, int64_t n, int32_t* colsum,
+                            hipStream_t st) {
+    hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, packed, kp, ldk, n, colsum);
     return hipGetLastError();
 }
 

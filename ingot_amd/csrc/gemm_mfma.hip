@@ -85,6 +85,14 @@ __device__ __forceinline__ void dma_barrier() {
     __syncthreads();
 }
 
+// Smallest number of passes (a divisor of tm, at least 2) whose slice of
+// 16-row blocks, for all waves, fits in `room` bytes.
+constexpr int staging_passes(int tm, int bytes_per_block_row, int room) {
+    for (int np = 2; np <= tm; ++np)
+        if (tm % np == 0 && (tm / np) * bytes_per_block_row <= room) return np;
+    return tm;
+}
+
 // LDS chunk swizzle: 16-byte chunk c of tile row r is stored at position
 // c ^ swz(r). (r >> 1) & 7 makes the 16 rows a ds_read_b128 phase touches
 // land on 16 distinct 16-byte bank groups of a 256-byte bank line.
@@ -232,7 +240,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     // staged rows with row-contiguous 16-byte stores. Accumulators are only
     // indexed statically.
     constexpr int SP = WN + 4;  // staging pitch (elements)
-    constexpr int NP = (NW * (WM / 2) * SP * 4 <= STAGE) ? 2 : ((NW * (WM / 4) * SP * 4 <= STAGE) ? 4 : 8);
+    constexpr int NP = staging_passes(TM, NW * 16 * SP * 4, STAGE);
     constexpr int HR = WM / NP;  // rows per pass
     static_assert(TM % NP == 0 && NW * HR * SP * 4 <= STAGE, "staging must fit in one LDS stage");
     static_assert(WN % 4 == 0, "row width must be whole float4s");
@@ -307,8 +315,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
 // Tile configurations per kind. occupancy: workgroups per CU the LDS and
 // register footprint allow; eff: relative throughput per CU slot (measured
 // on MI355X for the bf16 kernel).
-const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.80f}, {128, 128, 2, 0.90f}, {128, 64, 2, 0.85f},
-                                {64, 64, 4, 0.45f}};
+const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128, 128, 2, 0.80f}, {128, 64, 2, 0.78f},
+                                {64, 64, 4, 0.45f}, {192, 256, 1, 0.95f}};
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 1.00f}, {128, 64, 2, 0.95f}, {64, 64, 4, 0.85f}};
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 1, 0.85f}, {64, 64, 2, 0.60f}};
 const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.90f}, {128, 64, 2, 0.85f}, {64, 64, 4, 0.45f}};
@@ -337,10 +345,11 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
         case KIND_BF16:
             switch (cfg) {
                 case 0: return launch_one<KIND_BF16, 256, 256, 2, 4>(a, batch, st);
-                case 1: return launch_one<KIND_BF16, 256, 192, 2, 2>(a, batch, st);
+                case 1: return launch_one<KIND_BF16, 256, 192, 2, 4>(a, batch, st);
                 case 2: return launch_one<KIND_BF16, 128, 128, 2, 2>(a, batch, st);
                 case 3: return launch_one<KIND_BF16, 128, 64, 2, 2>(a, batch, st);
                 case 4: return launch_one<KIND_BF16, 64, 64, 2, 2>(a, batch, st);
+                case 5: return launch_one<KIND_BF16, 192, 256, 2, 4>(a, batch, st);
             }
             break;
         case KIND_BF16X2:

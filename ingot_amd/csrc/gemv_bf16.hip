@@ -1,26 +1,27 @@
 // Decode GEMV for gfx950: y[m,n] = epilogue(Σ_k x[m,k]·W[n,k]) for M <= 16
-// rows of f32 activations against a packed bf16 weight [Np][Kp].
+// rows of f32 activations against a packed bf16 weight [Np][Kp]. Two kernels:
+// M <= 4 streams weight rows whole with VALU FMAs (gemv_rows_kernel, below);
+// M = 5..16 runs the MFMA kernel described here.
 //
 // HBM-bound: the weight is streamed exactly once with 16-byte loads, and all
 // of a wave's loads for a round are issued before any MFMA waits on them.
 // The products run on v_mfma_f32_16x16x32_bf16 with the weight as the first
-// operand (16 weight rows per wave) and the activations as the second
-// (up to 16 rows, zero beyond M). To keep f32 activation accuracy, each x is
-// split into bf16 hi + lo parts (hi = bf16(x), lo = bf16(x − hi); |x − hi −
-// lo| <= 2⁻¹⁷|x|) and both are multiplied: bf16×bf16 products are exact in
-// f32, so the only roundings are the f32 accumulations, as in the reference's
-// f32 dot (kernels/vek/vek_generic.go:183-190). Under INGOT_MATH_BF16
-// (split = 0) only the hi part is used: x rounded to bf16 once.
+// operand (16 weight rows) and the activations as the second (up to 16 rows,
+// zero beyond M). To keep f32 activation accuracy, each x is split into bf16
+// hi + lo parts (hi = bf16(x), lo = bf16(x − hi); |x − hi − lo| <= 2⁻¹⁷|x|)
+// and both are multiplied: bf16×bf16 products are exact in f32, so the only
+// roundings are the f32 accumulations, as in the reference's f32 dot
+// (kernels/vek/vek_generic.go:183-190). Under INGOT_MATH_BF16 (split = 0)
+// only the hi part is used: x rounded to bf16 once.
 //
-// Work split: a workgroup (4 waves) owns 64 weight rows and one K slice of
-// KS elements; the grid's y dimension splits K (wavefront split-K). Lane
-// (r, g) of a wave loads, per round, 8 consecutive 16-byte chunks of row r:
-// k = k0 + t·256 + g·64 + u·8 + [0, 8). The activation slice is staged once
-// per workgroup in LDS (hi and lo planes, padded rows) and read with the same
-// k mapping. With S > 1 the partial sums go to a scratch buffer and the last
-// workgroup of each row block (arrival counter) adds the S partials in fixed
-// order — deterministic, one launch — applies the epilogue and re-arms the
-// counter.
+// Work split: one workgroup per 16 weight rows; its NW waves split K
+// (wavefront split-K) by 256-wide rounds, round t going to wave t % NW. In a
+// round, lane (r, g) loads, for u = 0..7, the 16 bytes of row r at
+// k = t·256 + (u·4 + g)·8: every load instruction reads 64 contiguous bytes
+// of each of the 16 rows. Lanes r < M read the same k of activation row r
+// (f32, L2-resident) and split it in registers. The NW partial tiles are
+// added in wave order through LDS — deterministic, no cross-workgroup
+// traffic, no fences — and the epilogue runs on the sum.
 //
 // Reference counterparts: gemvBF16 / gemm.GemvBF16 (ops/matmul.go:177-190,
 // kernels/gemm/bgemm.go:201-206) and the Metal gemv_bf16 kernel
@@ -32,108 +33,219 @@ namespace ingot {
 
 namespace {
 
-constexpr int U = 8;        // 16-byte weight chunks per lane per round
-constexpr int KR = 32 * U;  // k per round per wave
+constexpr int KR = 256;  // k granularity of the packed weight
 
-__global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvArgs p) {
-    extern __shared__ __attribute__((aligned(16))) char xs_raw[];
-    __shared__ int s_last;
-    const int M = p.M;
-    const int KS = p.KS;
-    const int XP = KS + 8;  // padded LDS row (elements)
-    uint16_t* xhi = (uint16_t*)xs_raw;
-    uint16_t* xlo = xhi + M * XP;
-
-    const int rb = blockIdx.x, s = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int k0 = s * KS;
-
-    const uint16_t* wp = p.w + (int64_t)(rb * 64 + wave * 16 + r) * p.ldw + k0 + g * (8 * U);
-    i32x4_t w[U];
+__device__ __forceinline__ void split8(const float* v, i32x4_t& hi, i32x4_t& lo, bool split) {
+    uint16_t h[8], l[8];
 #pragma unroll
-    for (int u = 0; u < U; ++u) w[u] = *(const i32x4_t*)(wp + u * 8);
-
-    // stage x[0..M)[k0 .. k0+KS) as bf16 hi/lo planes
-    for (int idx = tid; idx < M * KS; idx += 256) {
-        const int m = idx / KS;
-        const int kk = idx - m * KS;
-        const int k = k0 + kk;
-        const float v = k < p.K ? p.x[(int64_t)m * p.ldx + k] : 0.f;
-        const uint16_t h = f32_to_bf16(v);
-        xhi[m * XP + kk] = h;
-        xlo[m * XP + kk] = p.split ? f32_to_bf16(v - bf16_to_f32(h)) : (uint16_t)0;
+    for (int e = 0; e < 8; ++e) {
+        h[e] = f32_to_bf16(v[e]);
+        l[e] = split ? f32_to_bf16(v[e] - bf16_to_f32(h[e])) : (uint16_t)0;
     }
-    __syncthreads();
+    __builtin_memcpy(&hi, h, 16);
+    __builtin_memcpy(&lo, l, 16);
+}
+
+// U: 16-byte weight chunks per lane per round (a round covers 32·U of k).
+template <int NW, int U>
+__global__ __launch_bounds__(64 * NW) void gemv_bf16_kernel(GemvArgs p) {
+    constexpr int RK = 32 * U;  // k per round
+    __shared__ f32x4_t red[NW][64];
+    const int rb = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int rounds = (int)(p.kp / RK);
+
+    const uint16_t* wrow = p.w + (int64_t)(rb * 16 + r) * p.ldw + g * 8;
+    const bool xrow = r < p.M;
+    const float* xr = p.x + (int64_t)(xrow ? r : 0) * p.ldx + g * 8;
 
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    const bool xrow = r < M;
-    const uint16_t* xh = xhi + (xrow ? r : 0) * XP + g * (8 * U);
-    const uint16_t* xl = xlo + (xrow ? r : 0) * XP + g * (8 * U);
-    const i32x4_t zero = {0, 0, 0, 0};
-    const int rounds = KS / KR;
-    for (int t = 0; t < rounds; ++t) {
-        const bool more = t + 1 < rounds;
-        i32x4_t wn[U];
-        if (more) {
+    for (int t = wave; t < rounds; t += NW) {
+        i32x4_t w[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) wn[u] = *(const i32x4_t*)(wp + (t + 1) * KR + u * 8);
+        for (int u = 0; u < U; ++u) w[u] = *(const i32x4_t*)(wrow + t * RK + u * 32);
+        float xv[U][8];
+        if (xrow) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k0 = t * RK + u * 32 + g * 8;
+                const float* src = xr + t * RK + u * 32;
+                if (p.x_vec && k0 + 8 <= p.K) {
+                    const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        xv[u][e] = a[e];
+                        xv[u][e + 4] = b[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) xv[u][e] = k0 + e < p.K ? src[e] : 0.f;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[u][e] = 0.f;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const i32x4_t h = xrow ? *(const i32x4_t*)(xh + t * KR + u * 8) : zero;
-            const i32x4_t l = xrow ? *(const i32x4_t*)(xl + t * KR + u * 8) : zero;
+            i32x4_t hi, lo;
+            split8(xv[u], hi, lo, p.split);
             const bf16x8_t wv = __builtin_bit_cast(bf16x8_t, w[u]);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, h), acc, 0, 0, 0);
-            if (p.split) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, l), acc, 0, 0, 0);
-        }
-        if (more) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) w[u] = wn[u];
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, hi), acc, 0, 0, 0);
+            if (p.split) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, lo), acc, 0, 0, 0);
         }
     }
 
-    // lane (r, g) holds y[m = r][n = nb + q], q = 0..3
-    const int nloc = wave * 16 + 4 * g;
-    if (p.S == 1) {
-        if (xrow) {
+    // lane (r, g) holds y[m = r][n = rb·16 + 4g + q], q = 0..3
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0 || !xrow) return;
+    f32x4_t sum = red[0][lane];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int n = rb * 64 + nloc + q;
-                if (n < p.N) p.y[(int64_t)r * p.ldy + n] = epi_apply(p.epi, acc[q], r, n);
-            }
-        }
-        return;
+    for (int v = 1; v < NW; ++v) sum += red[v][lane];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int n = rb * 16 + 4 * g + q;
+        if (n < p.N) p.y[(int64_t)r * p.ldy + n] = epi_apply(p.epi, sum[q], r, n);
     }
-
-    float* part = p.part + (int64_t)(rb * p.S + s) * M * 64;
-    if (xrow) *(f32x4_t*)(part + r * 64 + nloc) = acc;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&p.cnt[rb], 1u) == (unsigned)(p.S - 1);
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const float* pb = p.part + (int64_t)rb * p.S * M * 64;
-    for (int idx = tid; idx < M * 64; idx += 256) {
-        const int m = idx >> 6;
-        const int n = rb * 64 + (idx & 63);
-        float sum = 0.f;
-        for (int s2 = 0; s2 < p.S; ++s2)
-            sum += __hip_atomic_load(pb + (s2 * M + m) * 64 + (idx & 63), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (n < p.N) p.y[(int64_t)m * p.ldy + n] = epi_apply(p.epi, sum, m, n);
-    }
-    if (tid == 0) __hip_atomic_store(&p.cnt[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
 
-hipError_t launch_gemv_bf16(const GemvArgs& a, hipStream_t st) {
-    if (a.KS % KR != 0 || a.M < 1 || a.M > 16) return hipErrorInvalidValue;
-    dim3 grid((a.N + 63) / 64, a.S);
-    const size_t lds = (size_t)a.M * (a.KS + 8) * 2 * sizeof(uint16_t);
-    hipLaunchKernelGGL(gemv_bf16_kernel, grid, dim3(256), lds, st, a);
+// ---- M <= 4: rows streamed whole by VALU FMAs ----
+// A wave owns R weight rows and walks K in 512-wide chunks: lane l reads the
+// 16 bytes at k = c·512 + 8l of each row (1 KiB contiguous per row per load
+// instruction) and the matching 8 f32 activations of each of the MM rows, and
+// accumulates in f32. The 64 lane partials of each output are then added by a
+// fixed butterfly (deterministic). x stays f32 (the reference's f32 dot),
+// except under INGOT_MATH_BF16 (split = 0), where it is rounded to bf16 once.
+template <int R, int MM>
+__global__ __launch_bounds__(256) void gemv_rows_kernel(GemvArgs p) {
+    constexpr int CH = MM >= 4 ? 2 : 4;  // chunks in flight per step
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = (blockIdx.x * 4 + wave) * R;
+    if (row0 >= p.N) return;
+    const int chunks = (int)((p.kp + 511) / 512);
+    float acc[R][MM];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) acc[r][m] = 0.f;
+
+    for (int c0 = 0; c0 < chunks; c0 += CH) {
+        i32x4_t w[CH][R];
+        float xv[CH][MM][8];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int k0 = (c0 + c) * 512 + lane * 8;
+            const bool win = c0 + c < chunks && k0 < p.kp;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                w[c][r] = win ? *(const i32x4_t*)(p.w + (int64_t)(row0 + r) * p.ldw + k0) : i32x4_t{0, 0, 0, 0};
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                const float* src = p.x + (int64_t)m * p.ldx + k0;
+                if (m < p.M && win && p.x_vec && k0 + 8 <= p.K) {
+                    const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        xv[c][m][e] = a[e];
+                        xv[c][m][e + 4] = b[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) xv[c][m][e] = (m < p.M && win && k0 + e < p.K) ? src[e] : 0.f;
+                }
+            }
+        }
+        if (!p.split) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+#pragma unroll
+                for (int m = 0; m < MM; ++m)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) xv[c][m][e] = bf16_to_f32(f32_to_bf16(xv[c][m][e]));
+        }
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t* wb = (const uint32_t*)&w[c][r];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float lo = __uint_as_float(wb[e] << 16);
+                    const float hi = __uint_as_float(wb[e] & 0xFFFF0000u);
+#pragma unroll
+                    for (int m = 0; m < MM; ++m) {
+                        acc[r][m] = fmaf(xv[c][m][2 * e], lo, acc[r][m]);
+                        acc[r][m] = fmaf(xv[c][m][2 * e + 1], hi, acc[r][m]);
+                    }
+                }
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            float v = acc[r][m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            acc[r][m] = v;
+        }
+    if (lane != 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int n = row0 + r;
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+            if (m < p.M) p.y[(int64_t)m * p.ldy + n] = epi_apply(p.epi, acc[r][m], m, n);
+    }
+}
+
+template <int R, int MM>
+hipError_t launch_rows(const GemvArgs& a, hipStream_t st) {
+    const int waves = (a.N + R - 1) / R;
+    hipLaunchKernelGGL((gemv_rows_kernel<R, MM>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
     return hipGetLastError();
+}
+
+template <int NW, int U>
+hipError_t launch_cfg(const GemvArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((gemv_bf16_kernel<NW, U>), dim3((a.N + 15) / 16), dim3(64 * NW), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st) {
+    if (a.kp % KR != 0 || a.M < 1 || a.M > 16) return hipErrorInvalidValue;
+    if (cfg == 0) {  // default: rows kernel for M <= 4, MFMA kernel above
+        if (a.M == 1) return launch_rows<1, 1>(a, st);
+        if (a.M == 2) return launch_rows<1, 2>(a, st);
+        if (a.M <= 4) return launch_rows<1, 4>(a, st);
+        return launch_cfg<8, 2>(a, st);
+    }
+    switch (cfg) {
+        case 10: return launch_rows<1, 1>(a, st);
+        case 11: return launch_rows<2, 1>(a, st);
+        case 12: return launch_rows<4, 1>(a, st);
+        case 13: return launch_rows<1, 4>(a, st);
+        case 14: return launch_rows<2, 4>(a, st);
+        case 15: return launch_rows<1, 2>(a, st);
+        case 20: return launch_cfg<8, 8>(a, st);
+        case 1: return launch_cfg<4, 8>(a, st);
+        case 2: return launch_cfg<8, 4>(a, st);
+        case 3: return launch_cfg<4, 4>(a, st);
+        case 4: return launch_cfg<2, 8>(a, st);
+        case 5: return launch_cfg<4, 2>(a, st);
+        case 6: return launch_cfg<16, 4>(a, st);
+        case 7: return launch_cfg<8, 2>(a, st);
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace ingot

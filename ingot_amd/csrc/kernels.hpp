@@ -52,26 +52,27 @@ struct GemvArgs {
     const float* x;
     int64_t ldx;
     int M, K;
-    const uint16_t* w;   // packed bf16 [>= 64·ceil(N/64)][ldw]
+    int x_vec;           // x rows 16-byte aligned (vector loads allowed)
+    const uint16_t* w;   // packed bf16 [>= 16·ceil(N/16)][ldw]
     int64_t ldw;
+    int64_t kp;          // padded K (multiple of 256)
     int N;
-    int S;               // k splits
     int split;           // 1: x as bf16 hi + lo (f32-class); 0: x rounded to bf16 once
-    int KS;              // k per split (multiple of 256)
-    float* part;         // S > 1: partial sums [ceil(N/64)][S][M][64]
-    unsigned* cnt;       // S > 1: zeroed arrival counters, one per 64-row block
     Epi epi;
     float* y;
     int64_t ldy;
 };
-hipError_t launch_gemv_bf16(const GemvArgs& a, hipStream_t st);
+// cfg selects (waves per workgroup, 16-byte chunks per lane per round).
+hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st);
 
 // Packs a weight into [np][kp] of dst_kind, zero padded. src_dtype is an
 // INGOT_DT_* code; trans = 1: src is [n][k] (row pitch ld), 0: src is [k][n].
+// Rows of dst are ldk elements apart (ldk >= kp).
 hipError_t launch_pack_weight(const void* src, int src_dtype, int64_t ld, int trans, int64_t n, int64_t k,
-                              void* dst, GemmKind dst_kind, int64_t np, int64_t kp, hipStream_t st);
-// colsum[j] = Σ_k packed[j][k] over an int8 packed weight.
-hipError_t launch_colsum_i8(const int8_t* packed, int64_t kp, int64_t n, int32_t* colsum, hipStream_t st);
+                              void* dst, GemmKind dst_kind, int64_t np, int64_t kp, int64_t ldk, hipStream_t st);
+// colsum[j] = Σ_k packed[j][k] over an int8 packed weight (row pitch ldk).
+hipError_t launch_colsum_i8(const int8_t* packed, int64_t kp, int64_t ldk, int64_t n, int32_t* colsum,
+                            hipStream_t st);
 // Packs activations A[M][K] (or [K][M] when trans) into [M][kl] of dst_kind
 // (kl = whole k-tiles), batch items at src_stride / dst_stride elements.
 hipError_t launch_pack_a(const void* src, int src_dtype, int64_t lda, int trans, int64_t m, int64_t k,

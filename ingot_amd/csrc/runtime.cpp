@@ -347,19 +347,21 @@ static int weight_pack(ingot_rocm_session* s, int src_dtype, int pack_dtype, int
     w->k = k;
     w->np = round_up(n, 256);
     w->kp = round_up(k, 256);
+    // One extra 128-byte line per row keeps rows off a power-of-two stride.
+    w->ldk = w->kp + 128 / kind_size(kind);
     const int esz = elem_size(src_dtype);
     const size_t src_bytes = (size_t)((rows - 1) * ld + cols) * esz;
     const void* dsrc = src;
     void* tmp = nullptr;
-    hipError_t e = hipMalloc(&w->data, (size_t)(w->np * w->kp) * kind_size(kind));
+    hipError_t e = hipMalloc(&w->data, (size_t)(w->np * w->ldk) * kind_size(kind));
     if (e == hipSuccess && kind == KIND_I8) e = hipMalloc((void**)&w->colsum, sizeof(int32_t) * w->np);
     if (e == hipSuccess && host) {
         e = hipMalloc(&tmp, src_bytes);
         if (e == hipSuccess) e = hipMemcpyAsync(tmp, src, src_bytes, hipMemcpyHostToDevice, s->stream);
         dsrc = tmp;
     }
-    if (e == hipSuccess) e = launch_pack_weight(dsrc, src_dtype, ld, trans, n, k, w->data, kind, w->np, w->kp, s->stream);
-    if (e == hipSuccess && kind == KIND_I8) e = launch_colsum_i8((const int8_t*)w->data, w->kp, w->np, w->colsum, s->stream);
+    if (e == hipSuccess) e = launch_pack_weight(dsrc, src_dtype, ld, trans, n, k, w->data, kind, w->np, w->kp, w->ldk, s->stream);
+    if (e == hipSuccess && kind == KIND_I8) e = launch_colsum_i8((const int8_t*)w->data, w->kp, w->ldk, w->np, w->colsum, s->stream);
     if (host && e == hipSuccess) e = hipStreamSynchronize(s->stream);
     if (tmp) (void)hipFree(tmp);
     if (e != hipSuccess) {
@@ -409,44 +411,24 @@ int ingot_rocm_weight_info(const ingot_rocm_weight* w, int64_t* n, int64_t* k, i
 
 static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     const ingot_rocm_weight* w = a->w;
-    const int M = (int)a->M;
-    const int64_t RB = (a->N + 63) / 64;
-    const int64_t KT = w->kp / 256;
-    if (RB > ingot_rocm_session::kCounters) return fail(INGOT_EDECLINED, "gemv: N %lld too large", (long long)a->N);
-    // K slice bound by LDS: M·(KS+8)·4 bytes of staged activations <= 64 KiB.
-    const int64_t kmax = std::max<int64_t>(256, (16384 / M - 8) / 256 * 256);
-    int64_t target = (int64_t)s->num_cus * 4;
-    if (const char* t = getenv("INGOT_GEMV_TARGET")) target = std::max(1, atoi(t));
-    int64_t S = 0;
-    for (int64_t d = 1; d <= KT; ++d) {
-        if (KT % d) continue;
-        if (w->kp / d > kmax) continue;
-        if (S == 0 || RB * d <= target) S = d;
-    }
-    if (S == 0) S = KT;
     GemvArgs g;
+    memset(&g, 0, sizeof g);
     g.x = (const float*)a->d_a;
     g.ldx = a->lda;
-    g.M = M;
+    g.M = (int)a->M;
     g.K = (int)a->K;
+    g.x_vec = aligned16(a->d_a) && (a->lda % 4) == 0;
     g.w = (const uint16_t*)w->data;
-    g.ldw = w->kp;
+    g.ldw = w->ldk;
+    g.kp = w->kp;
     g.N = (int)a->N;
-    g.S = (int)S;
     g.split = a->math == INGOT_MATH_BF16 ? 0 : 1;
-    g.KS = (int)(w->kp / S);
-    g.part = nullptr;
-    g.cnt = s->counters;
     g.epi = make_epi(a);
     g.y = a->d_y;
     g.ldy = a->ldy;
-    if (S > 1) {
-        void* ws;
-        int rc = ws_reserve(s, (size_t)RB * S * M * 64 * sizeof(float), &ws);
-        if (rc) return rc;
-        g.part = (float*)ws;
-    }
-    hipError_t e = launch_gemv_bf16(g, s->stream);
+    int cfg = 0;
+    if (const char* f = getenv("INGOT_GEMV_CFG")) cfg = atoi(f);
+    hipError_t e = launch_gemv_bf16(g, cfg, s->stream);
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return INGOT_OK;
 }
@@ -509,7 +491,7 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     GemmArgs g;
     memset(&g, 0, sizeof g);
     // Every GEMM operand is addressed with 32-bit buffer offsets.
-    const int64_t b_extent = w->np * w->kp * esz;
+    const int64_t b_extent = w->np * w->ldk * esz;
     const int64_t a_extent = direct ? (a->M - 1) * a->lda * a_esz + kl * esz : (int64_t)planes * a->M * kl * esz;
     if (b_extent >= ((int64_t)1 << 31) || a_extent >= ((int64_t)1 << 31))
         return fail(INGOT_EDECLINED, "gemm: operand larger than 2 GiB");
@@ -533,7 +515,7 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
         g.a_plane_bytes = plane * esz;
     }
     g.b = (const char*)w->data;
-    g.ldb_bytes = w->kp * esz;
+    g.ldb_bytes = w->ldk * esz;
     g.M = (int)a->M;
     g.N = (int)a->N;
     g.kt = (int)(kl * esz / KTILE_BYTES);
@@ -575,10 +557,10 @@ int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64
     GemmArgs g;
     memset(&g, 0, sizeof g);
     const int64_t a_extent = direct ? (M - 1) * lda + kl : M * kl;
-    if (w->np * w->kp >= ((int64_t)1 << 31) || a_extent >= ((int64_t)1 << 31))
+    if (w->np * w->ldk >= ((int64_t)1 << 31) || a_extent >= ((int64_t)1 << 31))
         return fail(INGOT_EDECLINED, "matmul_integer: operand larger than 2 GiB");
     g.a_bytes = (uint32_t)a_extent;
-    g.b_bytes = (uint32_t)(w->np * w->kp);
+    g.b_bytes = (uint32_t)(w->np * w->ldk);
     if (direct) {
         g.a = (const char*)d_a;
         g.lda_bytes = lda;
@@ -593,7 +575,7 @@ int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64
         g.lda_bytes = kl;
     }
     g.b = (const char*)w->data;
-    g.ldb_bytes = w->kp;
+    g.ldb_bytes = w->ldk;
     g.M = (int)M;
     g.N = (int)N;
     g.kt = (int)(kl / KTILE_BYTES);

@@ -13,6 +13,7 @@ struct ingot_rocm_weight {
     ingot::GemmKind kind;
     int64_t n, k;            // logical [n][k]
     int64_t np, kp;          // packed [np][kp], zero padded to multiples of 256
+    int64_t ldk;             // row pitch in elements (>= kp)
     void* data;
     int32_t* colsum;         // int8 weights: Σ_k W[n][k]
 };
