@@ -108,7 +108,8 @@ class Dit:
         achieved = flops / (ms * 1e-3) / 1e12
         return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK["bf16"], "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK["bf16"], 4), "traffic": None,
-                "kernel": "gemm_kernel<bf16,256,192>", "avg_launch_us": round(ms * 1e3, 2),
+                "kernel": "gemm_kernel<bf16> (256x192 for QKV and MLP-down, 256x256 for MLP-up)",
+                "avg_launch_us": round(ms * 1e3, 2),
                 "flops_per_launch": flops}
 
     def cpu_baseline(self, threads: int, seconds: float):
