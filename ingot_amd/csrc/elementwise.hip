@@ -76,17 +76,18 @@ __device__ __forceinline__ float load_a(const char* sb, int src_dt, int trans, i
 template <int KD>
 __global__ void pack_a_kernel(const void* src, int src_dt, int64_t lda, int trans, int64_t m, int64_t k,
                               int64_t src_stride, void* dst, int64_t kl, int64_t dst_stride, int64_t plane) {
+    // grid: x over the 16-byte chunks of a row, y over rows (strided), z over batch items
     constexpr int EPC = KD == KIND_F32 ? 4 : (KD == KIND_I8 ? 16 : 8);  // elements per chunk
     const int64_t chunks_per_row = kl / EPC;
-    const int64_t total = m * chunks_per_row;
-    const int b = blockIdx.y;
+    const int64_t cc = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (cc >= chunks_per_row) return;
+    const int b = blockIdx.z;
     const char* sb = (const char*)src;
     const int esz = src_dt == INGOT_DT_F32 ? 4 : (src_dt == INGOT_DT_BF16 ? 2 : 1);
     sb += (int64_t)b * src_stride * esz;
     const int esz_d = KD == KIND_F32 ? 4 : (KD == KIND_I8 ? 1 : 2);
-    for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < total; c += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t row = c / chunks_per_row;
-        const int64_t k0 = (c - row * chunks_per_row) * EPC;
+    const int64_t k0 = cc * EPC;
+    for (int64_t row = blockIdx.y; row < m; row += gridDim.y) {
         char* db = (char*)dst + ((int64_t)b * dst_stride + row * kl + k0) * esz_d;
         if (KD == KIND_I8) {
             uint8_t v[16];
@@ -194,7 +195,8 @@ hipError_t launch_pack_a(const void* src, int src_dtype, int64_t lda, int trans,
                          int64_t src_stride, void* dst, GemmKind dst_kind, int64_t kl, int64_t dst_stride, int batch,
                          hipStream_t st) {
     const int epc = dst_kind == KIND_F32 ? 4 : (dst_kind == KIND_I8 ? 16 : 8);
-    dim3 grid(grid_for(m * (kl / epc), 256), batch);
+    const int64_t chunks = kl / epc;
+    dim3 grid((unsigned)((chunks + 255) / 256), (unsigned)(m < 65535 ? (m > 0 ? m : 1) : 65535), batch);
     const int64_t plane = m * kl;
     switch (dst_kind) {
         case KIND_BF16:

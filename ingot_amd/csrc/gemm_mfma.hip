@@ -78,11 +78,28 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 #define LDS_AS(ptr) ((__attribute__((address_space(3))) void*)(ptr))
 
 // The workgroup barrier does not wait for LDS-DMA loads (they count as
-// vector-memory loads, not LDS stores), so every wave drains its own DMA and
-// LDS traffic first: s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(0).
-__device__ __forceinline__ void dma_barrier() {
-    __builtin_amdgcn_s_waitcnt(0x0070);
-    __syncthreads();
+// vector-memory loads, not LDS stores), so before it every wave waits until at
+// most `groups` of its k-tile DMA groups (G instructions each) are in flight,
+// and for all its LDS reads: s_waitcnt vmcnt(groups·G) expcnt(7) lgkmcnt(0).
+// DMA groups complete in issue order, so the oldest ones are the ones done.
+template <int V>
+__device__ __forceinline__ void waitcnt_vm() {
+    static_assert(V >= 0 && V < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | 0x70);
+}
+
+template <int G, int NS>
+__device__ __forceinline__ void wait_dma_groups(int groups) {
+    static_assert((NS - 1) * G < 64, "outstanding DMA must fit the 6-bit vmcnt");
+    switch (groups) {
+        case 0: waitcnt_vm<0>(); break;
+        case 1: waitcnt_vm<(NS > 1 ? 1 : 0) * G>(); break;
+        case 2: waitcnt_vm<(NS > 2 ? 2 : 0) * G>(); break;
+        case 3: waitcnt_vm<(NS > 3 ? 3 : 0) * G>(); break;
+        case 4: waitcnt_vm<(NS > 4 ? 4 : 0) * G>(); break;
+        case 5: waitcnt_vm<(NS > 5 ? 5 : 0) * G>(); break;
+        default: waitcnt_vm<0>(); break;
+    }
 }
 
 // Smallest number of passes (a divisor of tm, at least 2) whose slice of
@@ -98,7 +115,7 @@ constexpr int staging_passes(int tm, int bytes_per_block_row, int room) {
 // land on 16 distinct 16-byte bank groups of a 256-byte bank line.
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
-template <int KD, int BM, int BN, int WGM, int WGN>
+template <int KD, int BM, int BN, int WGM, int WGN, int NS>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     constexpr bool SPLIT = KD == KIND_BF16X2;
     constexpr int AP = SPLIT ? 2 : 1;  // activation planes
@@ -111,11 +128,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     static_assert(BM % 32 == 0 && BN % 32 == 0, "tile must be a multiple of 32");
     typedef typename AccOf<KD>::type Acc;
 
-    // Two LDS stages, separate objects so the compiler can tell a stage being
-    // filled by DMA from the one being read. Rows are 128 bytes, unpadded; the
-    // 16-byte chunk c of row r sits at position c ^ (r % 8).
-    __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
-    __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
+    // NS LDS stages (a ring of k-tiles). Rows are 128 bytes, unpadded; the
+    // 16-byte chunk c of row r sits at position c ^ swz(r).
+    static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "LDS ring must fit in 160 KiB");
+    __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -210,28 +226,36 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
                 for (int j = 0; j < TN; ++j) mma16<KD>(acc[i][j], fb[j], fa[pl][i]);
     };
 
-    // Software pipeline over k-tiles, two LDS stages and two fragment sets.
-    // The k-tile's second-half fragments are read while its first half is
-    // multiplied; the barrier sits between the halves (all reads of the
-    // stage are done, the next stage's DMA has landed); right after it the
-    // stage just consumed is refilled two k-tiles ahead and the next
-    // k-tile's first-half fragments are read while the second half is
-    // multiplied.
+    // Software pipeline over k-tiles: an NS-stage LDS ring filled by DMA NS
+    // k-tiles ahead, and two fragment register sets. A k-tile's second-half
+    // fragments are read while its first half is multiplied; the barrier sits
+    // between the halves (every wave has read the stage; k-tile kt+1 has
+    // landed); right after it the consumed stage is refilled with k-tile
+    // kt+NS and the next k-tile's first-half fragments are read while the
+    // second half is multiplied. Before the barrier each wave waits only until
+    // the DMA groups issued after k-tile kt+1's are the ones still in flight.
+    constexpr int G = AP * IA + IB;  // DMA instructions per wave per k-tile
     FragA fa0, fa1;
     FragB fb0, fb1;
-    dma(lds0, 0);
-    if (p.kt > 1) dma(lds1, 1);
-    dma_barrier();  // k-tile 0 (and 1) in LDS
-    read_frags(lds0, 0, fa0, fb0);
-    for (int kt = 0; kt < p.kt; ++kt) {
-        char* cur = (kt & 1) ? lds1 : lds0;
-        char* nxt = (kt & 1) ? lds0 : lds1;
+    const int KT = p.kt;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+        if (s < KT) dma(lds + s * STAGE, s);
+    wait_dma_groups<G, NS>(min(NS, KT) - 1);
+    __syncthreads();  // k-tile 0 in LDS
+    read_frags(lds, 0, fa0, fb0);
+    int st = 0;  // ring slot of k-tile kt
+    for (int kt = 0; kt < KT; ++kt) {
+        char* cur = lds + st * STAGE;
+        const int st1 = st + 1 == NS ? 0 : st + 1;
         read_frags(cur, 1, fa1, fb1);
         mma_all(fa0, fb0);
-        dma_barrier();  // cur fully read by every wave; k-tile kt+1 landed in nxt
-        if (kt + 2 < p.kt) dma(cur, kt + 2);
-        if (kt + 1 < p.kt) read_frags(nxt, 0, fa0, fb0);
+        wait_dma_groups<G, NS>(max(0, min(NS - 2, KT - 2 - kt)));
+        __syncthreads();  // cur fully read by every wave; k-tile kt+1 landed
+        if (kt + NS < KT) dma(cur, kt + NS);
+        if (kt + 1 < KT) read_frags(lds + st1 * STAGE, 0, fa0, fb0);
         mma_all(fa1, fb1);
+        st = st1;
     }
 
     // ---- epilogue ----
@@ -240,11 +264,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     // staged rows with row-contiguous 16-byte stores. Accumulators are only
     // indexed statically.
     constexpr int SP = WN + 4;  // staging pitch (elements)
-    constexpr int NP = staging_passes(TM, NW * 16 * SP * 4, STAGE);
+    constexpr int NP = staging_passes(TM, NW * 16 * SP * 4, NS * STAGE);
     constexpr int HR = WM / NP;  // rows per pass
-    static_assert(TM % NP == 0 && NW * HR * SP * 4 <= STAGE, "staging must fit in one LDS stage");
+    static_assert(TM % NP == 0 && NW * HR * SP * 4 <= NS * STAGE, "staging must fit in the LDS ring");
     static_assert(WN % 4 == 0, "row width must be whole float4s");
-    char* stage = lds0 + wave * (HR * SP * 4);
+    char* stage = lds + wave * (HR * SP * 4);
     const int r = lane & 15;
     const int g4 = (lane >> 4) * 4;
     const int row0 = m0 + wm * WM;
@@ -315,16 +339,18 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
 // Tile configurations per kind. occupancy: workgroups per CU the LDS and
 // register footprint allow; eff: relative throughput per CU slot (measured
 // on MI355X for the bf16 kernel).
-const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128, 128, 2, 0.80f}, {128, 64, 2, 0.78f},
-                                {64, 64, 4, 0.45f}, {192, 256, 1, 0.95f}};
-const GemmConfig kF32Cfgs[] = {{128, 128, 2, 1.00f}, {128, 64, 2, 0.95f}, {64, 64, 4, 0.85f}};
-const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 1, 0.85f}, {64, 64, 2, 0.60f}};
-const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.90f}, {128, 64, 2, 0.85f}, {64, 64, 4, 0.45f}};
+// Small tiles keep two LDS stages: at these sizes occupancy (more resident
+// workgroups) hides latency better than a deeper ring (measured on MI355X).
+const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128, 128, 2, 0.80f}, {128, 64, 3, 0.78f},
+                                {64, 64, 4, 0.60f}, {192, 256, 1, 0.95f}};
+const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}};
+const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}};
+const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f}};
 
-template <int KD, int BM, int BN, int WGM, int WGN>
+template <int KD, int BM, int BN, int WGM, int WGN, int NS>
 hipError_t launch_one(const GemmArgs& a, int batch, hipStream_t st) {
     dim3 grid(a.tiles_m * a.tiles_n, batch);
-    hipLaunchKernelGGL((gemm_kernel<KD, BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), 0, st, a);
+    hipLaunchKernelGGL((gemm_kernel<KD, BM, BN, WGM, WGN, NS>), grid, dim3(64 * WGM * WGN), 0, st, a);
     return hipGetLastError();
 }
 
@@ -344,34 +370,34 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
     switch (kind) {
         case KIND_BF16:
             switch (cfg) {
-                case 0: return launch_one<KIND_BF16, 256, 256, 2, 4>(a, batch, st);
-                case 1: return launch_one<KIND_BF16, 256, 192, 2, 4>(a, batch, st);
-                case 2: return launch_one<KIND_BF16, 128, 128, 2, 2>(a, batch, st);
-                case 3: return launch_one<KIND_BF16, 128, 64, 2, 2>(a, batch, st);
-                case 4: return launch_one<KIND_BF16, 64, 64, 2, 2>(a, batch, st);
-                case 5: return launch_one<KIND_BF16, 192, 256, 2, 4>(a, batch, st);
+                case 0: return launch_one<KIND_BF16, 256, 256, 2, 4, 2>(a, batch, st);
+                case 1: return launch_one<KIND_BF16, 256, 192, 2, 4, 2>(a, batch, st);
+                case 2: return launch_one<KIND_BF16, 128, 128, 2, 2, 2>(a, batch, st);
+                case 3: return launch_one<KIND_BF16, 128, 64, 2, 2, 2>(a, batch, st);
+                case 4: return launch_one<KIND_BF16, 64, 64, 2, 2, 2>(a, batch, st);
+                case 5: return launch_one<KIND_BF16, 192, 256, 2, 4, 2>(a, batch, st);
             }
             break;
         case KIND_BF16X2:
             switch (cfg) {
-                case 0: return launch_one<KIND_BF16X2, 128, 128, 2, 2>(a, batch, st);
-                case 1: return launch_one<KIND_BF16X2, 128, 64, 2, 2>(a, batch, st);
-                case 2: return launch_one<KIND_BF16X2, 64, 64, 2, 2>(a, batch, st);
+                case 0: return launch_one<KIND_BF16X2, 128, 128, 2, 2, 2>(a, batch, st);
+                case 1: return launch_one<KIND_BF16X2, 128, 64, 2, 2, 2>(a, batch, st);
+                case 2: return launch_one<KIND_BF16X2, 64, 64, 2, 2, 2>(a, batch, st);
             }
             break;
         case KIND_F32:
             switch (cfg) {
-                case 0: return launch_one<KIND_F32, 128, 128, 2, 2>(a, batch, st);
-                case 1: return launch_one<KIND_F32, 128, 64, 2, 2>(a, batch, st);
-                case 2: return launch_one<KIND_F32, 64, 64, 2, 2>(a, batch, st);
+                case 0: return launch_one<KIND_F32, 128, 128, 2, 2, 2>(a, batch, st);
+                case 1: return launch_one<KIND_F32, 128, 64, 2, 2, 2>(a, batch, st);
+                case 2: return launch_one<KIND_F32, 64, 64, 2, 2, 2>(a, batch, st);
             }
             break;
         case KIND_I8:
             switch (cfg) {
-                case 0: return launch_one<KIND_I8, 256, 256, 2, 4>(a, batch, st);
-                case 1: return launch_one<KIND_I8, 128, 128, 2, 2>(a, batch, st);
-                case 2: return launch_one<KIND_I8, 128, 64, 2, 2>(a, batch, st);
-                case 3: return launch_one<KIND_I8, 64, 64, 2, 2>(a, batch, st);
+                case 0: return launch_one<KIND_I8, 256, 256, 2, 4, 2>(a, batch, st);
+                case 1: return launch_one<KIND_I8, 128, 128, 2, 2, 2>(a, batch, st);
+                case 2: return launch_one<KIND_I8, 128, 64, 2, 2, 2>(a, batch, st);
+                case 3: return launch_one<KIND_I8, 64, 64, 2, 2, 2>(a, batch, st);
             }
             break;
     }
