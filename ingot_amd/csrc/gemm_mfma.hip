@@ -15,15 +15,15 @@
 // The weight is the first MFMA operand (rows n) and A the second (rows m):
 // D[n][m] lands in lane (m%16, n/4) as 4 consecutive n.
 //
-// Workgroup: 256 threads = 4 waves in a 2×2 grid, each wave a
-// (BM/2)×(BN/2) sub-tile of 16×16 MFMA blocks, accumulators in AGPRs. A and B
-// k-tiles move global → LDS by DMA (buffer_load_dwordx4 ... lds): no staging
-// registers, 32-bit buffer offsets, hardware zero-fill past the operand end.
-// Two LDS stages: the next k-tile's DMA is in flight while the current one is
-// multiplied, one barrier per k-tile. Tile order is XCD-aware (consecutive
-// tiles of the grouped order run on one XCD's L2) and grouped by GROUP_M tile
-// rows. The epilogue (bias/C, activation, post scale/shift, or the int8
-// column-sum correction + dequant) runs on the staged accumulators.
+// Workgroup: WGM×WGN waves (4 or 8), each a (BM/WGM)×(BN/WGN) sub-tile of
+// 16×16 MFMA blocks. A and B k-tiles move global → LDS by DMA
+// (buffer_load_dwordx4 ... lds): no staging registers, 32-bit range-checked
+// buffer offsets, hardware zero-fill past the operand end. An NS-stage LDS
+// ring keeps NS-1 k-tiles of DMA in flight while one is multiplied; one
+// barrier per k-tile. Tile order is XCD-aware (consecutive tiles of the
+// grouped order run on one XCD's L2) and grouped by GROUP_M tile rows. The
+// epilogue (bias/C, activation, post scale/shift, or the int8 column-sum
+// correction + dequant) runs on the accumulators staged through LDS.
 //
 // Reference counterparts: the packed-B sweep + micro-kernel of
 // kernels/gemm/gemm.go:280-334,431-490 (f32), PackBBF16/widenPanel
@@ -102,6 +102,27 @@ __device__ __forceinline__ void wait_dma_groups(int groups) {
     }
 }
 
+// Scheduling template for one half k-step of NM MFMAs, NV DMA loads and ND
+// LDS fragment reads: after MFMA i come the next ceil((NV+ND)/NM) memory
+// instructions (DMA first), so every load is issued early in the half and the
+// remaining MFMAs cover its latency. Instruction classes of
+// sched_group_barrier: 0x008 MFMA, 0x020 VMEM read, 0x100 DS read.
+template <int NM, int NV, int ND, int I = 0>
+__device__ __forceinline__ void interleave() {
+    if constexpr (I < NM) {
+        constexpr int NMEM = NV + ND;
+        constexpr int R = (NMEM + NM - 1) / NM;
+        constexpr int lo = I * R < NMEM ? I * R : NMEM;
+        constexpr int hi = (I + 1) * R < NMEM ? (I + 1) * R : NMEM;
+        constexpr int v = (hi < NV ? hi : NV) - (lo < NV ? lo : NV);
+        constexpr int d = (hi - lo) - v;
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x020, v, 0);
+        if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);
+        interleave<NM, NV, ND, I + 1>();
+    }
+}
+
 // Smallest number of passes (a divisor of tm, at least 2) whose slice of
 // 16-row blocks, for all waves, fits in `room` bytes.
 constexpr int staging_passes(int tm, int bytes_per_block_row, int room) {
@@ -168,22 +189,30 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
         voff_b[h] = (uint32_t)(lr * p.ldb_bytes) + (uint32_t)(c << 4);
     }
 
+    // The whole byte offset (row, plane, k-tile, lane chunk) goes in the
+    // range-checked VGPR offset; the SGPR offset stays 0. A k-tile index past
+    // the end gets offset 2^31 + row offset (< 2^32, above every extent: the
+    // host keeps row offsets below 2^31), so its load fetches nothing and
+    // writes zeros: the pipeline below issues one DMA group per k-tile
+    // unconditionally.
+    const int KT = p.kt;
     auto dma = [&](char* st, int kt) {
-        const uint32_t kofs = (uint32_t)kt * KTILE_BYTES;
+        const uint32_t kofs = kt < KT ? (uint32_t)kt * KTILE_BYTES : 0x80000000u;
 #pragma unroll
         for (int pl = 0; pl < AP; ++pl)
 #pragma unroll
             for (int j = 0; j < IA; ++j) {
                 const int r = (j * NW + wave) * 8;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rsa, LDS_AS(st + (pl * BM + r) * KTILE_BYTES), 16, voff_a[(r >> 3) & 1],
-                    (uint32_t)((m0 + r) * p.lda_bytes + pl * p.a_plane_bytes) + kofs, 0, 0);
+                const uint32_t row = (uint32_t)((m0 + r) * p.lda_bytes + pl * p.a_plane_bytes) + kofs;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, LDS_AS(st + (pl * BM + r) * KTILE_BYTES), 16,
+                                                         voff_a[(r >> 3) & 1] + row, 0, 0, 0);
             }
 #pragma unroll
         for (int j = 0; j < IB; ++j) {
             const int r = (j * NW + wave) * 8;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, LDS_AS(st + (AP * BM + r) * KTILE_BYTES), 16, voff_b[(r >> 3) & 1],
-                                                     (uint32_t)((n0 + r) * p.ldb_bytes) + kofs, 0, 0);
+            const uint32_t row = (uint32_t)((n0 + r) * p.ldb_bytes) + kofs;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, LDS_AS(st + (AP * BM + r) * KTILE_BYTES), 16,
+                                                     voff_b[(r >> 3) & 1] + row, 0, 0, 0);
         }
     };
 
@@ -232,16 +261,21 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     // between the halves (every wave has read the stage; k-tile kt+1 has
     // landed); right after it the consumed stage is refilled with k-tile
     // kt+NS and the next k-tile's first-half fragments are read while the
-    // second half is multiplied. Before the barrier each wave waits only until
-    // the DMA groups issued after k-tile kt+1's are the ones still in flight.
-    constexpr int G = AP * IA + IB;  // DMA instructions per wave per k-tile
+    // second half is multiplied. Exactly one DMA group is issued per k-tile
+    // (past the end: out of range, see dma), so before the barrier each wave
+    // waits until at most the NS-2 groups issued after k-tile kt+1's are in
+    // flight. The loop body has no branches, so each half is one scheduling
+    // region: its memory instructions are spread between its MFMAs
+    // (interleave) and sched_barriers keep the wait and the barrier after
+    // the half's last MFMA.
+    constexpr int G = AP * IA + IB;                                   // DMA instructions per wave per k-tile
+    constexpr int NFR = AP * TM + TN;                                 // LDS fragment reads per half
+    constexpr int NMF = (KD == KIND_F32 ? 4 : 1) * AP * TM * TN;      // MFMAs per half
     FragA fa0, fa1;
     FragB fb0, fb1;
-    const int KT = p.kt;
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-        if (s < KT) dma(lds + s * STAGE, s);
-    wait_dma_groups<G, NS>(min(NS, KT) - 1);
+    for (int s = 0; s < NS; ++s) dma(lds + s * STAGE, s);
+    wait_dma_groups<G, NS>(NS - 1);
     __syncthreads();  // k-tile 0 in LDS
     read_frags(lds, 0, fa0, fb0);
     int st = 0;  // ring slot of k-tile kt
@@ -250,13 +284,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
         const int st1 = st + 1 == NS ? 0 : st + 1;
         read_frags(cur, 1, fa1, fb1);
         mma_all(fa0, fb0);
-        wait_dma_groups<G, NS>(max(0, min(NS - 2, KT - 2 - kt)));
+        interleave<NMF, 0, NFR>();
+        __builtin_amdgcn_sched_barrier(0);
+        wait_dma_groups<G, NS>(NS - 2);
         __syncthreads();  // cur fully read by every wave; k-tile kt+1 landed
-        if (kt + NS < KT) dma(cur, kt + NS);
-        if (kt + 1 < KT) read_frags(lds + st1 * STAGE, 0, fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        dma(cur, kt + NS);
+        read_frags(lds + st1 * STAGE, 0, fa0, fb0);  // after the last k-tile: unused
         mma_all(fa1, fb1);
+        interleave<NMF, G, NFR>();
+        __builtin_amdgcn_sched_barrier(0);
         st = st1;
     }
+    // The tail's out-of-range DMA groups and fragment reads finish before the
+    // epilogue reuses the ring.
+    waitcnt_vm<0>();
+    __syncthreads();
 
     // ---- epilogue ----
     // Each wave stages a slice of its sub-tile at a time through its own part

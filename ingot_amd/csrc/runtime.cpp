@@ -491,9 +491,12 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     GemmArgs g;
     memset(&g, 0, sizeof g);
     // Every GEMM operand is addressed with 32-bit buffer offsets.
+    // Row offsets of a whole tile past the last row (256 rows) must stay below
+    // 2^31 too: the kernel marks past-the-end k-tiles by adding 2^31.
     const int64_t b_extent = w->np * w->ldk * esz;
-    const int64_t a_extent = direct ? (a->M - 1) * a->lda * a_esz + kl * esz : (int64_t)planes * a->M * kl * esz;
-    if (b_extent >= ((int64_t)1 << 31) || a_extent >= ((int64_t)1 << 31))
+    const int64_t a_pitch = direct ? a->lda * a_esz : kl * esz;
+    const int64_t a_extent = direct ? (a->M - 1) * a_pitch + kl * esz : (int64_t)planes * a->M * kl * esz;
+    if (b_extent + 256 * w->ldk * esz >= ((int64_t)1 << 31) || a_extent + 256 * a_pitch >= ((int64_t)1 << 31))
         return fail(INGOT_EDECLINED, "gemm: operand larger than 2 GiB");
     g.a_bytes = (uint32_t)a_extent;
     g.b_bytes = (uint32_t)b_extent;
@@ -556,8 +559,9 @@ int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64
     const bool direct = K % 128 == 0 && lda % 16 == 0 && aligned16(d_a);
     GemmArgs g;
     memset(&g, 0, sizeof g);
+    const int64_t a_pitch = direct ? lda : kl;
     const int64_t a_extent = direct ? (M - 1) * lda + kl : M * kl;
-    if (w->np * w->ldk >= ((int64_t)1 << 31) || a_extent >= ((int64_t)1 << 31))
+    if ((w->np + 256) * w->ldk >= ((int64_t)1 << 31) || a_extent + 256 * a_pitch >= ((int64_t)1 << 31))
         return fail(INGOT_EDECLINED, "matmul_integer: operand larger than 2 GiB");
     g.a_bytes = (uint32_t)a_extent;
     g.b_bytes = (uint32_t)(w->np * w->ldk);
