@@ -31,6 +31,8 @@
 // kernels/gemm/qgemm.go:246-320 (int8), and the bias/act store epilogue of
 // SgemmPackedBEpi kernels/gemm/gemm.go:521-597.
 
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace ingot {
@@ -121,14 +123,6 @@ __device__ __forceinline__ void interleave() {
         if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);
         interleave<NM, NV, ND, I + 1>();
     }
-}
-
-// Smallest number of passes (a divisor of tm, at least 2) whose slice of
-// 16-row blocks, for all waves, fits in `room` bytes.
-constexpr int staging_passes(int tm, int bytes_per_block_row, int room) {
-    for (int np = 2; np <= tm; ++np)
-        if (tm % np == 0 && (tm / np) * bytes_per_block_row <= room) return np;
-    return tm;
 }
 
 // LDS chunk swizzle: 16-byte chunk c of tile row r is stored at position
@@ -296,26 +290,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
         __builtin_amdgcn_sched_barrier(0);
         st = st1;
     }
-    // The tail's out-of-range DMA groups and fragment reads finish before the
-    // epilogue reuses the ring.
+    // The tail's out-of-range DMA groups land before the workgroup ends (its
+    // LDS may be handed to the next workgroup).
     waitcnt_vm<0>();
-    __syncthreads();
 
-    // ---- epilogue ----
-    // Each wave stages a slice of its sub-tile at a time through its own part
-    // of lds0: lanes write their 4-wide column strips, then the wave walks the
-    // staged rows with row-contiguous 16-byte stores. Accumulators are only
-    // indexed statically.
-    constexpr int SP = WN + 4;  // staging pitch (elements)
-    constexpr int NP = staging_passes(TM, NW * 16 * SP * 4, NS * STAGE);
-    constexpr int HR = WM / NP;  // rows per pass
-    static_assert(TM % NP == 0 && NW * HR * SP * 4 <= NS * STAGE, "staging must fit in the LDS ring");
-    static_assert(WN % 4 == 0, "row width must be whole float4s");
-    char* stage = lds + wave * (HR * SP * 4);
+    // ---- epilogue: straight from the accumulators ----
+    // Lane (r, g) holds Y[m][n..n+3] of each 16×16 block (m = block row + r,
+    // n = block column + 4g): one 16-byte store per block, 16 rows × 64 bytes
+    // per store instruction. Each epilogue step is a wave-uniform branch
+    // around an unrolled pass over all accumulators, so accumulators are only
+    // indexed statically and the per-element code is branch-free.
     const int r = lane & 15;
     const int g4 = (lane >> 4) * 4;
-    const int row0 = m0 + wm * WM;
-    const int col0 = n0 + wn * WN;
+    const int row0 = m0 + wm * WM + r;
+    const int col0 = n0 + wn * WN + g4;
     const int64_t ybatch = (int64_t)blockIdx.y * p.stride_y;
     // 16-byte stores need an aligned row start (n is always a multiple of 4 here)
     uintptr_t ybase;
@@ -324,34 +312,33 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     else
         ybase = (uintptr_t)((float*)p.y + ybatch);
     const bool vec_ok = (ybase & 15) == 0 && (p.ldy & 3) == 0;
+
+    if constexpr (KD == KIND_I8) {
+        const QEpi& q = p.qepi;
 #pragma unroll
-    for (int h = 0; h < NP; ++h) {
+        for (int j = 0; j < TN; ++j) {
+            const int n = col0 + j * 16;
+            if (n >= p.N) continue;
+            int32_t corr[4];
+            float sc[4];
 #pragma unroll
-        for (int i = 0; i < TM / NP; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                *(Acc*)(stage + ((i * 16 + r) * SP + j * 16 + g4) * 4) = acc[h * (TM / NP) + i][j];
-        __syncthreads();
-        constexpr int Q = WN / 4;  // float4 per staged row
-        for (int idx = lane; idx < HR * Q; idx += 64) {
-            const int rr = idx / Q;
-            const int cc = (idx - rr * Q) * 4;
-            const int m = row0 + h * HR + rr;
-            const int n = col0 + cc;
-            if (m >= p.M || n >= p.N) continue;
-            const Acc a4 = *(const Acc*)(stage + (rr * SP + cc) * 4);
-            const int64_t o = ybatch + (int64_t)m * p.ldy + n;
+            for (int e = 0; e < 4; ++e) {
+                const int nn = min(n + e, p.N - 1);
+                corr[e] = wrap_mul(q.colsum[nn], q.neg_za);
+                sc[e] = q.yf ? q.scale[q.n_scale == 1 ? 0 : nn] : 0.f;
+            }
             const bool full = n + 3 < p.N;
-            if (KD == KIND_I8) {
-                const QEpi& q = p.qepi;
-                const i32x4_t ai = __builtin_bit_cast(i32x4_t, a4);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int m = row0 + i * 16;
+                if (m >= p.M) continue;
+                const int64_t o = ybatch + (int64_t)m * p.ldy + n;
                 int32_t v[4];
                 float f[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int nn = min(n + e, p.N - 1);
-                    v[e] = wrap_add(ai[e], wrap_mul(q.colsum[nn], q.neg_za));
-                    f[e] = q.yf ? (float)wrap_add(v[e], -q.dq_zp) * q.scale[q.n_scale == 1 ? 0 : nn] : 0.f;
+                    v[e] = wrap_add(acc[i][j][e], corr[e]);
+                    f[e] = (float)wrap_add(v[e], -q.dq_zp) * sc[e];
                 }
                 if (full && vec_ok) {
                     if (q.yi) *(i32x4_t*)(q.yi + o) = i32x4_t{v[0], v[1], v[2], v[3]};
@@ -362,20 +349,84 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
                         if (q.yf) q.yf[o + e] = f[e];
                     }
                 }
-            } else {
-                float* y = (float*)p.y;
-                const f32x4_t af = __builtin_bit_cast(f32x4_t, a4);
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = epi_apply(p.epi, af[e], m, min(n + e, p.N - 1));
-                if (full && vec_ok) {
-                    *(f32x4_t*)(y + o) = f32x4_t{v[0], v[1], v[2], v[3]};
-                } else {
-                    for (int e = 0; e < 4 && n + e < p.N; ++e) y[o + e] = v[e];
-                }
             }
         }
-        __syncthreads();
+    } else {
+        // v = post(act(alpha·acc + beta·C)): the C term is split into a
+        // per-column part (C_ROW, C_SCALAR), a per-row part (C_COL) and a
+        // per-element load (C_FULL); absent terms are −0.0, the exact
+        // additive identity (x + −0 = x, signed zeros included), and an
+        // absent post step is ·1 + −0. One activation switch around
+        // straight-line code keeps accumulators out of branch joins.
+        const Epi& e = p.epi;
+        const float nz = -0.0f;
+        f32x4_t cn[TN];
+        float cm[TM];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) cn[j] = f32x4_t{nz, nz, nz, nz};
+#pragma unroll
+        for (int i = 0; i < TM; ++i) cm[i] = nz;
+        if (e.c_mode == INGOT_C_ROW) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) cn[j][q] = e.beta * e.c[min(col0 + j * 16 + q, p.N - 1)];
+        } else if (e.c_mode == INGOT_C_SCALAR) {
+            const float c0 = e.beta * e.c[0];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) cn[j] = f32x4_t{c0, c0, c0, c0};
+        } else if (e.c_mode == INGOT_C_COL) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) cm[i] = e.beta * e.c[min(row0 + i * 16, p.M - 1)];
+        }
+        const bool cfull = e.c_mode == INGOT_C_FULL;
+        const float ps = e.post ? e.post_scale : 1.f, pt = e.post ? e.post_shift : nz;
+        float* y = (float*)p.y;
+        auto store_all = [&](auto act) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int m = row0 + i * 16;
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int n = col0 + j * 16;
+                    f32x4_t c4 = cn[j];
+                    if (cfull) {
+                        const int64_t mc = min(m, p.M - 1);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) c4[q] = e.beta * e.c[mc * e.ldc + min(n + q, p.N - 1)];
+                    }
+                    f32x4_t v;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float x = e.alpha * acc[i][j][q] + c4[q] + cm[i];
+                        v[q] = apply_act(x, decltype(act)::value, e.act_alpha, e.act_beta) * ps + pt;
+                    }
+                    if (m < p.M && n < p.N) {
+                        const int64_t o = ybatch + (int64_t)m * p.ldy + n;
+                        if (n + 3 < p.N && vec_ok) {
+                            *(f32x4_t*)(y + o) = v;
+                        } else {
+                            for (int q = 0; q < 4 && n + q < p.N; ++q) y[o + q] = v[q];
+                        }
+                    }
+                }
+            }
+        };
+        switch (e.act) {
+#define INGOT_ACT_CASE(A) \
+    case A: store_all(std::integral_constant<int, A>()); break;
+            INGOT_ACT_CASE(INGOT_ACT_RELU)
+            INGOT_ACT_CASE(INGOT_ACT_GELU_ERF)
+            INGOT_ACT_CASE(INGOT_ACT_GELU_TANH)
+            INGOT_ACT_CASE(INGOT_ACT_SIGMOID)
+            INGOT_ACT_CASE(INGOT_ACT_SILU)
+            INGOT_ACT_CASE(INGOT_ACT_HARDSWISH)
+            INGOT_ACT_CASE(INGOT_ACT_HARDSIGMOID)
+            INGOT_ACT_CASE(INGOT_ACT_CLIP)
+            INGOT_ACT_CASE(INGOT_ACT_LEAKYRELU)
+#undef INGOT_ACT_CASE
+            default: store_all(std::integral_constant<int, INGOT_ACT_NONE>()); break;
+        }
     }
 }
 
@@ -385,7 +436,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
 // Small tiles keep two LDS stages: at these sizes occupancy (more resident
 // workgroups) hides latency better than a deeper ring (measured on MI355X).
 const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128, 128, 2, 0.80f}, {128, 64, 3, 0.78f},
-                                {64, 64, 4, 0.60f}, {192, 256, 1, 0.95f}};
+                                {64, 64, 4, 0.60f}, {192, 256, 1, 0.95f}, {256, 256, 1, 0.01f}, {256, 128, 1, 0.01f}, {256, 128, 1, 0.01f}};
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}};
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}};
 const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f}};
@@ -419,6 +470,9 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 3: return launch_one<KIND_BF16, 128, 64, 2, 2, 2>(a, batch, st);
                 case 4: return launch_one<KIND_BF16, 64, 64, 2, 2, 2>(a, batch, st);
                 case 5: return launch_one<KIND_BF16, 192, 256, 2, 4, 2>(a, batch, st);
+                case 6: return launch_one<KIND_BF16, 256, 256, 2, 2, 2>(a, batch, st);
+                case 7: return launch_one<KIND_BF16, 256, 128, 4, 2, 2>(a, batch, st);
+                case 8: return launch_one<KIND_BF16, 256, 128, 4, 2, 3>(a, batch, st);
             }
             break;
         case KIND_BF16X2:
