@@ -16,7 +16,11 @@ Cache, serves them).
 
 roofline: the dominant kernel's algorithmic FLOPs (or bytes) per launch over
 its average launch duration, timed with HIP events on the session stream
-(the stream the kernels run on). cpu_baseline: the reference's amd64 CPU
+(the stream the kernels run on). roofline.traffic is the kernel's HBM bytes
+per launch as counted by rocprofv3 (FETCH_SIZE + WRITE_SIZE, each scaled by
+what the counter reads for a plain copy of known size) over `bench.py
+--probe`; the summary, with its commands, is profiles/dit_gemm_traffic.md,
+and bench.py reads the figure from there. cpu_baseline: the reference's amd64 CPU
 algorithm restated in C++ (oracle/baseline.cpp, kind "port"), timed on a
 bounded row sample of the same workload on this host.
 """
@@ -35,6 +39,20 @@ sys.path.insert(0, ROOT)
 
 METRIC = "GEMM TFLOPS (bf16/fp32), int8 TOPS, GEMV HBM GB/s; % of MI355X roofline"
 PEAK = {"bf16": 2516.6, "f32": 157.3, "i8": 5033.2, "hbm": 8000.0}  # TFLOP/s, TOP/s, GB/s
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "dit_gemm_traffic.md")
+PROBE_COPY_BYTES = 256 << 20
+
+
+def measured_traffic():
+    """HBM bytes per DiT GEMM launch from the committed rocprofv3 summary, or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("bytes_per_launch ="):
+                    return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg: str) -> None:
@@ -107,10 +125,24 @@ class Dit:
             t.free()
         achieved = flops / (ms * 1e-3) / 1e12
         return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK["bf16"], "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK["bf16"], 4), "traffic": None,
+                "frac": round(achieved / PEAK["bf16"], 4), "traffic": measured_traffic(),
                 "kernel": "gemm_kernel<bf16> (256x192 for QKV and MLP-down, 256x256 for MLP-up)",
                 "avg_launch_us": round(ms * 1e3, 2),
                 "flops_per_launch": flops}
+
+    def probe(self):
+        """One plain copy of PROBE_COPY_BYTES (counter calibration), then one launch of each GEMM."""
+        L, s = self.L, self.sess
+        src, dst = s.empty(L.DT_U8, (PROBE_COPY_BYTES,)), s.empty(L.DT_U8, (PROBE_COPY_BYTES,))
+        s.memset(src, 1)
+        s.copy_d2d(dst, src)
+        a16 = {}
+        for k, t in self.a.items():
+            a16[k] = s.empty(L.DT_BF16, (self.M, k))
+            s.cast_bf16(t, a16[k])
+        for (k, n, _), w, y, act in zip(self.shapes, self.w, self.y, self.acts):
+            s.gemm(a16[k], w, y, self.M, act=act, a_dtype=L.DT_BF16)
+        s.sync()
 
     def cpu_baseline(self, threads: int, seconds: float):
         import oracle
@@ -250,6 +282,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="measure only the headline workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--probe", action="store_true",
+                    help="counter probe for rocprofv3 --pmc: one calibration copy + one launch of each DiT GEMM")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU (the path has no multi-GPU component); run with --gpus 1")
@@ -259,6 +293,10 @@ def main() -> int:
     from ingot_amd import _lib as L
 
     sess = Session(0)
+    if args.probe:
+        Dit(sess, L).probe()
+        sess.close()
+        return 0
     res = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
     if args.workload == "dit":

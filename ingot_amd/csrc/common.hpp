@@ -48,12 +48,29 @@ __device__ __forceinline__ float exp_clamped(float x) {
 
 __device__ __forceinline__ float clamp01(float x) { return fminf(fmaxf(x, 0.f), 1.f); }
 
+// erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7), the approximation
+// the reference's amd64 GELU kernel evaluates (kernels/vek/genamd64/main.go:62-99):
+//   erf(|z|) = 1 − t·(a1 + t·(a2 + t·(a3 + t·(a4 + t·a5))))·e^(−z²),
+//   t = 1 / (1 + p·|z|), odd in z.
+// The reciprocal and the exponential are the hardware ones (v_rcp_f32,
+// v_exp_f32, about 1 ulp), far inside the formula's own error.
+__device__ __forceinline__ float erf_as(float z) {
+    const float az = fabsf(z);
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, az, 1.f));
+    float poly = fmaf(1.061405429f, t, -1.453152027f);
+    poly = fmaf(poly, t, 1.421413741f);
+    poly = fmaf(poly, t, -0.284496736f);
+    poly = fmaf(poly, t, 0.254829592f);
+    const float r = 1.f - poly * t * __expf(-az * az);
+    return copysignf(r, z);
+}
+
 // Activation set of ops/epilogue.go:48-73 plus the GELU forms of
-// ops/elementwise.go:411-414 (tanh) and kernels/vek/vek_generic.go:165-170 (erf).
+// ops/elementwise.go:411-414 (tanh) and kernels/vek/vek_amd64.go:346-353 (erf).
 __device__ __forceinline__ float apply_act(float x, int act, float a, float b) {
     switch (act) {
         case INGOT_ACT_RELU: return fmaxf(x, 0.f);
-        case INGOT_ACT_GELU_ERF: return 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
+        case INGOT_ACT_GELU_ERF: return 0.5f * x * (1.f + erf_as(x * 0.70710678118654752f));
         case INGOT_ACT_GELU_TANH: {
             float u = x + 0.044715f * x * x * x;
             return 0.5f * x * (1.f + tanhf(0.7978845608028654f * u));

@@ -104,6 +104,17 @@ __device__ __forceinline__ void wait_dma_groups(int groups) {
     }
 }
 
+// Workgroup barrier of the k-loop. The waits it relies on (this wave's DMA
+// groups up to the needed k-tile, and its LDS reads) are issued explicitly
+// right before it, so it carries no memory fence: a workgroup release fence
+// would also wait for every LDS-DMA still in flight and drain the ring. The
+// empty asm statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void kloop_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Scheduling template for one half k-step of NM MFMAs, NV DMA loads and ND
 // LDS fragment reads: after MFMA i come the next ceil((NV+ND)/NM) memory
 // instructions (DMA first), so every load is issued early in the half and the
@@ -262,15 +273,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     // region: its memory instructions are spread between its MFMAs
     // (interleave) and sched_barriers keep the wait and the barrier after
     // the half's last MFMA.
-    constexpr int G = AP * IA + IB;                                   // DMA instructions per wave per k-tile
-    constexpr int NFR = AP * TM + TN;                                 // LDS fragment reads per half
-    constexpr int NMF = (KD == KIND_F32 ? 4 : 1) * AP * TM * TN;      // MFMAs per half
+    constexpr int G = AP * IA + IB;                               // DMA instructions per wave per k-tile
+    constexpr int NFR = AP * TM + TN;                             // LDS fragment reads per half
+    constexpr int NMF = (KD == KIND_F32 ? 4 : 1) * AP * TM * TN;  // MFMAs per half
     FragA fa0, fa1;
     FragB fb0, fb1;
 #pragma unroll
     for (int s = 0; s < NS; ++s) dma(lds + s * STAGE, s);
     wait_dma_groups<G, NS>(NS - 1);
-    __syncthreads();  // k-tile 0 in LDS
+    kloop_barrier();  // k-tile 0 in LDS
     read_frags(lds, 0, fa0, fb0);
     int st = 0;  // ring slot of k-tile kt
     for (int kt = 0; kt < KT; ++kt) {
@@ -281,7 +292,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
         interleave<NMF, 0, NFR>();
         __builtin_amdgcn_sched_barrier(0);
         wait_dma_groups<G, NS>(NS - 2);
-        __syncthreads();  // cur fully read by every wave; k-tile kt+1 landed
+        kloop_barrier();  // cur fully read by every wave; k-tile kt+1 landed
         __builtin_amdgcn_sched_barrier(0);
         dma(cur, kt + NS);
         read_frags(lds + st1 * STAGE, 0, fa0, fb0);  // after the last k-tile: unused
@@ -436,7 +447,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
 // Small tiles keep two LDS stages: at these sizes occupancy (more resident
 // workgroups) hides latency better than a deeper ring (measured on MI355X).
 const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128, 128, 2, 0.80f}, {128, 64, 3, 0.78f},
-                                {64, 64, 4, 0.60f}, {192, 256, 1, 0.95f}, {256, 256, 1, 0.01f}, {256, 128, 1, 0.01f}, {256, 128, 1, 0.01f}};
+                                {64, 64, 4, 0.60f}, {192, 256, 1, 0.95f}};
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}};
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}};
 const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f}};
@@ -464,15 +475,12 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
     switch (kind) {
         case KIND_BF16:
             switch (cfg) {
-                case 0: return launch_one<KIND_BF16, 256, 256, 2, 4, 2>(a, batch, st);
+                case 0: return launch_one<KIND_BF16, 256, 256, 4, 2, 2>(a, batch, st);
                 case 1: return launch_one<KIND_BF16, 256, 192, 2, 4, 2>(a, batch, st);
                 case 2: return launch_one<KIND_BF16, 128, 128, 2, 2, 2>(a, batch, st);
                 case 3: return launch_one<KIND_BF16, 128, 64, 2, 2, 2>(a, batch, st);
                 case 4: return launch_one<KIND_BF16, 64, 64, 2, 2, 2>(a, batch, st);
                 case 5: return launch_one<KIND_BF16, 192, 256, 2, 4, 2>(a, batch, st);
-                case 6: return launch_one<KIND_BF16, 256, 256, 2, 2, 2>(a, batch, st);
-                case 7: return launch_one<KIND_BF16, 256, 128, 4, 2, 2>(a, batch, st);
-                case 8: return launch_one<KIND_BF16, 256, 128, 4, 2, 3>(a, batch, st);
             }
             break;
         case KIND_BF16X2:

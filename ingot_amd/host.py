@@ -150,6 +150,14 @@ class Session:
             L.check(self.lib.ingot_rocm_memcpy_h2d(self.h, t.ptr, arr.ctypes.data, arr.nbytes))
         return t
 
+    def memset(self, t: DeviceTensor, value: int) -> None:
+        L.check(self.lib.ingot_rocm_memset(self.h, t.ptr, value, t.nbytes))
+
+    def copy_d2d(self, dst: DeviceTensor, src: DeviceTensor) -> None:
+        if dst.nbytes != src.nbytes:
+            raise ValueError(f"copy_d2d: {dst.nbytes} != {src.nbytes} bytes")
+        L.check(self.lib.ingot_rocm_memcpy_d2d(self.h, dst.ptr, src.ptr, src.nbytes))
+
     def sync(self) -> None:
         L.check(self.lib.ingot_rocm_sync(self.h))
 
