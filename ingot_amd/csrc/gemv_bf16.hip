@@ -6,22 +6,29 @@
 // HBM-bound: the weight is streamed exactly once with 16-byte loads, and all
 // of a wave's loads for a round are issued before any MFMA waits on them.
 // The products run on v_mfma_f32_16x16x32_bf16 with the weight as the first
-// operand (16 weight rows) and the activations as the second (up to 16 rows,
-// zero beyond M). To keep f32 activation accuracy, each x is split into bf16
-// hi + lo parts (hi = bf16(x), lo = bf16(x − hi); |x − hi − lo| <= 2⁻¹⁷|x|)
-// and both are multiplied: bf16×bf16 products are exact in f32, so the only
-// roundings are the f32 accumulations, as in the reference's f32 dot
+// operand (RB weight rows, the rest of the 16 zero) and the activations as
+// the second (16 rows, zero beyond M). To keep f32 activation accuracy, x is
+// split once per call, before this kernel, into bf16 hi + lo planes
+// (hi = bf16(x), lo = bf16(x − hi); |x − hi − lo| <= 2⁻¹⁷|x|) and both are
+// multiplied: bf16×bf16 products are exact in f32, so the only roundings are
+// the f32 accumulations, as in the reference's f32 dot
 // (kernels/vek/vek_generic.go:183-190). Under INGOT_MATH_BF16 (split = 0)
-// only the hi part is used: x rounded to bf16 once.
+// only the hi plane is used: x rounded to bf16 once. The planes are
+// written by pack_x_kernel in MFMA fragment order — for each 32-wide k step
+// the 16 rows × 32 k form 1 KiB in lane order (lane 16g + r: row r, k =
+// 32s + 8g .. +7; rows >= M zero) — so each x load instruction of this
+// kernel reads 1 KiB contiguous. Every workgroup reads all of x (twice the
+// weight bytes it streams, with both planes): converting it per workgroup
+// cost about five VALU operations per weight byte, and reading it with the
+// weight's 16-rows × 64-byte pattern bound the kernel on address traffic.
 //
-// Work split: one workgroup per 16 weight rows; its NW waves split K
-// (wavefront split-K) by 256-wide rounds, round t going to wave t % NW. In a
-// round, lane (r, g) loads, for u = 0..7, the 16 bytes of row r at
-// k = t·256 + (u·4 + g)·8: every load instruction reads 64 contiguous bytes
-// of each of the 16 rows. Lanes r < M read the same k of activation row r
-// (f32, L2-resident) and split it in registers. The NW partial tiles are
-// added in wave order through LDS — deterministic, no cross-workgroup
-// traffic, no fences — and the epilogue runs on the sum.
+// Work split: one workgroup per RB weight rows (RB = 8 keeps 256 workgroups
+// busy at N = 2048); its NW waves split K by rounds of 32·U, round t going
+// to wave t % NW. In a round, lane (r, g) loads, for u = 0..U-1, the 16
+// bytes of weight row r (r < RB) at k = t·32U + 32u + 8g and its own 16
+// bytes of x step t·U + u in both planes. The NW partial tiles are added in wave order through LDS —
+// deterministic, no cross-workgroup traffic, no fences — and the epilogue
+// runs on the sum.
 //
 // Reference counterparts: gemvBF16 / gemm.GemvBF16 (ops/matmul.go:177-190,
 // kernels/gemm/bgemm.go:201-206) and the Metal gemv_bf16 kernel
@@ -35,20 +42,35 @@ namespace {
 
 constexpr int KR = 256;  // k granularity of the packed weight
 
-__device__ __forceinline__ void split8(const float* v, i32x4_t& hi, i32x4_t& lo, bool split) {
-    uint16_t h[8], l[8];
+// x (f32 [M][ldx]) → bf16 planes in MFMA fragment order: 16-byte chunk c is
+// step s = c / 64, lane l = c % 64 (row r = l % 16, k = 32s + 8(l / 16));
+// rows >= M and k >= K are zero. hi = bf16(x) RNE; lo = bf16(x − hi).
+__global__ void pack_x_kernel(const float* x, int64_t ldx, int M, int K, int64_t chunks, int split, uint16_t* dst,
+                              int64_t plane) {
+    const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    const int l = (int)(c & 63);
+    const int r = l & 15;
+    const int64_t k0 = (c >> 6) * 32 + (l >> 4) * 8;
+    uint16_t h[8], lo[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        h[e] = f32_to_bf16(v[e]);
-        l[e] = split ? f32_to_bf16(v[e] - bf16_to_f32(h[e])) : (uint16_t)0;
+        const float v = (r < M && k0 + e < K) ? x[(int64_t)r * ldx + k0 + e] : 0.f;
+        h[e] = f32_to_bf16(v);
+        lo[e] = f32_to_bf16(v - bf16_to_f32(h[e]));
     }
-    __builtin_memcpy(&hi, h, 16);
-    __builtin_memcpy(&lo, l, 16);
+    i32x4_t o;
+    __builtin_memcpy(&o, h, 16);
+    *(i32x4_t*)(dst + c * 8) = o;
+    if (split) {
+        __builtin_memcpy(&o, lo, 16);
+        *(i32x4_t*)(dst + plane + c * 8) = o;
+    }
 }
 
-// U: 16-byte weight chunks per lane per round (a round covers 32·U of k).
-template <int NW, int U>
-__global__ __launch_bounds__(64 * NW) void gemv_bf16_kernel(GemvArgs p) {
+template <int NW, int U, int RB>
+__global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemvArgs p) {
+    static_assert(RB == 8 || RB == 16, "8 or 16 weight rows per workgroup");
     constexpr int RK = 32 * U;  // k per round
     __shared__ f32x4_t red[NW][64];
     const int rb = blockIdx.x;
@@ -57,59 +79,42 @@ __global__ __launch_bounds__(64 * NW) void gemv_bf16_kernel(GemvArgs p) {
     const int r = lane & 15, g = lane >> 4;
     const int rounds = (int)(p.kp / RK);
 
-    const uint16_t* wrow = p.w + (int64_t)(rb * 16 + r) * p.ldw + g * 8;
-    const bool xrow = r < p.M;
-    const float* xr = p.x + (int64_t)(xrow ? r : 0) * p.ldx + g * 8;
+    const bool wrow = r < RB;
+    const uint16_t* wrp = p.w + (int64_t)(rb * RB + (wrow ? r : 0)) * p.ldw + g * 8;
+    const i32x4_t* xh_p = (const i32x4_t*)p.xb + lane;
+    const i32x4_t* xl_p = (const i32x4_t*)(p.xb + p.xb_plane) + lane;
 
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     for (int t = wave; t < rounds; t += NW) {
-        i32x4_t w[U];
+        i32x4_t w[U], xh[U], xl[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) w[u] = *(const i32x4_t*)(wrow + t * RK + u * 32);
-        float xv[U][8];
-        if (xrow) {
+        for (int u = 0; u < U; ++u)
+            w[u] = wrow ? *(const i32x4_t*)(wrp + t * RK + u * 32) : i32x4_t{0, 0, 0, 0};
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int k0 = t * RK + u * 32 + g * 8;
-                const float* src = xr + t * RK + u * 32;
-                if (p.x_vec && k0 + 8 <= p.K) {
-                    const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        xv[u][e] = a[e];
-                        xv[u][e + 4] = b[e];
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) xv[u][e] = k0 + e < p.K ? src[e] : 0.f;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) xv[u][e] = 0.f;
+        for (int u = 0; u < U; ++u) {
+            const int64_t step = (int64_t)(t * U + u) * 64;
+            xh[u] = xh_p[step];
+            xl[u] = p.split ? xl_p[step] : i32x4_t{0, 0, 0, 0};
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            i32x4_t hi, lo;
-            split8(xv[u], hi, lo, p.split);
             const bf16x8_t wv = __builtin_bit_cast(bf16x8_t, w[u]);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, hi), acc, 0, 0, 0);
-            if (p.split) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, lo), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, xh[u]), acc, 0, 0, 0);
+            if (p.split)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, __builtin_bit_cast(bf16x8_t, xl[u]), acc, 0, 0, 0);
         }
     }
 
-    // lane (r, g) holds y[m = r][n = rb·16 + 4g + q], q = 0..3
+    // lane (r, g) holds y[m = r][n = rb·RB + 4g + q], q = 0..3
     red[wave][lane] = acc;
     __syncthreads();
-    if (wave != 0 || !xrow) return;
+    if (wave != 0 || r >= p.M || 4 * g >= RB) return;
     f32x4_t sum = red[0][lane];
 #pragma unroll
     for (int v = 1; v < NW; ++v) sum += red[v][lane];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int n = rb * 16 + 4 * g + q;
+        const int n = rb * RB + 4 * g + q;
         if (n < p.N) p.y[(int64_t)r * p.ldy + n] = epi_apply(p.epi, sum[q], r, n);
     }
 }
@@ -123,12 +128,12 @@ __global__ __launch_bounds__(64 * NW) void gemv_bf16_kernel(GemvArgs p) {
 // accumulates in f32. The 64 lane partials of each output are then added by a
 // fixed butterfly (deterministic). x stays f32 (the reference's f32 dot),
 // except under INGOT_MATH_BF16 (split = 0), where it is rounded to bf16 once.
-template <int R, int MM>
-__global__ __launch_bounds__(256) void gemv_rows_kernel(GemvArgs p) {
+template <int R, int MM, int WPB>
+__global__ __launch_bounds__(64 * WPB) void gemv_rows_kernel(GemvArgs p) {
     constexpr int CH = MM >= 4 ? 2 : 4;  // chunks in flight per step
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int row0 = (blockIdx.x * 4 + wave) * R;
+    const int row0 = (blockIdx.x * WPB + wave) * R;
     if (row0 >= p.N) return;
     const int chunks = (int)((p.kp + 511) / 512);
     float acc[R][MM];
@@ -208,42 +213,59 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(GemvArgs p) {
     }
 }
 
-template <int R, int MM>
+template <int R, int MM, int WPB = 4>
 hipError_t launch_rows(const GemvArgs& a, hipStream_t st) {
     const int waves = (a.N + R - 1) / R;
-    hipLaunchKernelGGL((gemv_rows_kernel<R, MM>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemv_rows_kernel<R, MM, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, st, a);
     return hipGetLastError();
 }
 
-template <int NW, int U>
-hipError_t launch_cfg(const GemvArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_bf16_kernel<NW, U>), dim3((a.N + 15) / 16), dim3(64 * NW), 0, st, a);
+hipError_t launch_pack_x(const float* x, int64_t ldx, int M, int K, int64_t kp, int split, uint16_t* dst,
+                        hipStream_t st) {
+    const int64_t chunks = kp / 32 * 64;  // 16 rows × kp / 8 elements per chunk
+    hipLaunchKernelGGL(pack_x_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st, x, ldx, M, K, chunks,
+                       split, dst, kp * 16);
+    return hipGetLastError();
+}
+
+template <int NW, int U, int RB>
+hipError_t launch_mfma(const GemvArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((gemv_mfma_kernel<NW, U, RB>), dim3((a.N + RB - 1) / RB), dim3(64 * NW), 0, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st) {
     if (a.kp % KR != 0 || a.M < 1 || a.M > 16) return hipErrorInvalidValue;
-    if (cfg == 0) {  // default: rows kernel for M <= 4, MFMA kernel above
+    if (a.M > 4 && !a.xb) return hipErrorInvalidValue;
+    if (cfg == 0) {  // default: rows kernel for M <= 4, MFMA kernel above (measured on MI355X)
         if (a.M == 1) return launch_rows<1, 1>(a, st);
         if (a.M == 2) return launch_rows<1, 2>(a, st);
-        if (a.M <= 4) return launch_rows<1, 4>(a, st);
-        return launch_cfg<8, 2>(a, st);
+        if (a.M <= 4) return a.N >= 4096 ? launch_rows<2, 4, 1>(a, st) : launch_rows<1, 4>(a, st);
+        return launch_mfma<8, 4, 16>(a, st);
+    }
+    if (a.M <= 4) {
+        switch (cfg) {
+            case 10: return launch_rows<1, 1>(a, st);
+            case 11: return launch_rows<2, 1>(a, st);
+            case 12: return launch_rows<4, 1>(a, st);
+            case 13: return launch_rows<1, 4>(a, st);
+            case 14: return launch_rows<2, 4>(a, st);
+            case 15: return launch_rows<1, 2>(a, st);
+            case 16: return launch_rows<4, 4, 1>(a, st);
+            case 17: return launch_rows<2, 4, 1>(a, st);
+            case 18: return launch_rows<4, 4, 2>(a, st);
+            case 19: return launch_rows<2, 2, 1>(a, st);
+        }
+        return hipErrorInvalidValue;
     }
     switch (cfg) {
-        case 10: return launch_rows<1, 1>(a, st);
-        case 11: return launch_rows<2, 1>(a, st);
-        case 12: return launch_rows<4, 1>(a, st);
-        case 13: return launch_rows<1, 4>(a, st);
-        case 14: return launch_rows<2, 4>(a, st);
-        case 15: return launch_rows<1, 2>(a, st);
-        case 20: return launch_cfg<8, 8>(a, st);
-        case 1: return launch_cfg<4, 8>(a, st);
-        case 2: return launch_cfg<8, 4>(a, st);
-        case 3: return launch_cfg<4, 4>(a, st);
-        case 4: return launch_cfg<2, 8>(a, st);
-        case 5: return launch_cfg<4, 2>(a, st);
-        case 6: return launch_cfg<16, 4>(a, st);
-        case 7: return launch_cfg<8, 2>(a, st);
+        case 1: return launch_mfma<8, 8, 16>(a, st);
+        case 2: return launch_mfma<8, 4, 8>(a, st);
+        case 3: return launch_mfma<4, 8, 8>(a, st);
+        case 4: return launch_mfma<4, 4, 8>(a, st);
+        case 5: return launch_mfma<16, 4, 8>(a, st);
+        case 6: return launch_mfma<8, 4, 16>(a, st);
+        case 7: return launch_mfma<4, 8, 16>(a, st);
     }
     return hipErrorInvalidValue;
 }

@@ -58,12 +58,20 @@ struct GemvArgs {
     int64_t kp;          // padded K (multiple of 256)
     int N;
     int split;           // 1: x as bf16 hi + lo (f32-class); 0: x rounded to bf16 once
+    // M > 4: x pre-packed by launch_pack_x as bf16 planes in MFMA fragment
+    // order (16 rows, zero padded; hi, then lo at +xb_plane when split).
+    const uint16_t* xb;
+    int64_t xb_plane;
     Epi epi;
     float* y;
     int64_t ldy;
 };
 // cfg selects (waves per workgroup, 16-byte chunks per lane per round).
 hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st);
+// x (f32 [M <= 16][ldx]) → the fragment-ordered bf16 planes the M > 4 GEMV
+// reads: dst holds (split ? 2 : 1) planes of 16·kp elements.
+hipError_t launch_pack_x(const float* x, int64_t ldx, int M, int K, int64_t kp, int split, uint16_t* dst,
+                         hipStream_t st);
 
 // Packs a weight into [np][kp] of dst_kind, zero padded. src_dtype is an
 // INGOT_DT_* code; trans = 1: src is [n][k] (row pitch ld), 0: src is [k][n].

@@ -426,6 +426,17 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     g.epi = make_epi(a);
     g.y = a->d_y;
     g.ldy = a->ldy;
+    if (a->M > 4) {
+        // the MFMA kernel reads x as fragment-ordered bf16 planes (hi, lo)
+        void* ws;
+        int rc = ws_reserve(s, (size_t)((g.split ? 2 : 1) * 16 * w->kp * 2), &ws);
+        if (rc) return rc;
+        hipError_t e = launch_pack_x((const float*)a->d_a, a->lda, (int)a->M, (int)a->K, w->kp, g.split,
+                                     (uint16_t*)ws, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "gemv pack x");
+        g.xb = (const uint16_t*)ws;
+        g.xb_plane = 16 * w->kp;
+    }
     int cfg = 0;
     if (const char* f = getenv("INGOT_GEMV_CFG")) cfg = atoi(f);
     hipError_t e = launch_gemv_bf16(g, cfg, s->stream);

@@ -177,10 +177,11 @@ def test_gemv_bf16_decode(sess, m, n, k):
     w.free()
 
 
-def test_gemv_epilogue(sess):
-    announce("gemv epilogue")
+@pytest.mark.parametrize("m", [3, 9])
+def test_gemv_epilogue(sess, m):
+    announce(f"gemv epilogue m={m}")
     rng = np.random.default_rng(5)
-    m, n, k = 3, 300, 1024
+    n, k = 300, 1024
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
     wb = bf16_weights(rng, (n, k), 0.02, "normal")
     bias = rng.normal(0, 0.1, n).astype(np.float32)
@@ -191,6 +192,37 @@ def test_gemv_epilogue(sess):
     want = oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16, alpha=0.5, beta=2.0, c=bias, c_mode=2,
                        act_code=L.ACT_SILU)
     assert_close(y.numpy(), want, nstar_tol(k, x, oracle.bf16_to_f32(wb)), "gemv epilogue")
+
+
+@pytest.mark.parametrize("cfg", ["10", "11", "12", "13", "14", "15", "16", "17", "18", "19",
+                                 "1", "2", "3", "4", "5", "6", "7"])
+@pytest.mark.parametrize("m", [1, 2, 4, 9, 16])
+def test_gemv_forced_configs(sess, monkeypatch, cfg, m):
+    """Every GEMV launch configuration (INGOT_GEMV_CFG) that applies to M, strided x, both math modes."""
+    rows_cfg = int(cfg) >= 10
+    mm = {"10": 1, "11": 1, "12": 1, "13": 4, "14": 4, "15": 2, "16": 4, "17": 4, "18": 4, "19": 2}.get(cfg, 16)
+    if (m > 4) == rows_cfg or m > mm:
+        pytest.skip("configuration does not cover this M")
+    announce(f"gemv cfg={cfg} m={m}")
+    monkeypatch.setenv("INGOT_GEMV_CFG", cfg)
+    rng = np.random.default_rng(int(cfg) * 31 + m)
+    n, k, lda = 328, 1300, 1309
+    xs = rng.normal(0, 1, (m, lda)).astype(np.float32)
+    x = xs[:, :k]
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    dx = sess.to_device(xs)
+    wide = oracle.bf16_to_f32(wb)
+    for math_mode in (L.MATH_AUTO, L.MATH_BF16):
+        y = sess.empty(L.DT_F32, (m, n))
+        sess.gemv_bf16(dx, w, y, m, lda=lda, math=math_mode)
+        xin = x if math_mode == L.MATH_AUTO else oracle.bf16_to_f32(oracle.f32_to_bf16(x))
+        want = oracle.gemm(np.ascontiguousarray(xin), wb, trans_b=True, b_dtype=oracle.BF16)
+        assert_close(y.numpy(), want, nstar_tol(k, x, wide), f"gemv cfg {cfg} m {m} math {math_mode}")
+        if math_mode == L.MATH_AUTO:
+            rel = np.max(np.abs(y.numpy() - want)) / max(1.0, np.max(np.abs(want)))
+            assert rel <= 1e-5 * math.sqrt(k), f"gemv cfg {cfg} relative error {rel:.3e}"
+    w.free()
 
 
 # ---------------- BASELINE configs at full size ----------------
