@@ -6,7 +6,7 @@
  *
  * Two layers are exported.
  *
- *  1. Kernel layer (ingot_rocm_gemm, ingot_rocm_gemv_bf16,
+ *  1. Kernel layer (ingot_rocm_gemm, ingot_rocm_gemm_dynamic_b, ingot_rocm_gemv_bf16,
  *     ingot_rocm_matmul_integer, ingot_rocm_dequantize_linear, ...). Plain
  *     device pointers and sizes. This is what a Go `rocm` backend binds with
  *     cgo, one call per gpuOp.prepare encoding
@@ -200,6 +200,17 @@ typedef struct ingot_rocm_gemm_args {
 } ingot_rocm_gemm_args;
 
 int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* args);
+
+/* Batched GEMM whose B is an activation: each batch item i multiplies its A
+ * (stride_a) by its own B at d_b + i·stride_b elements (stride_b 0: one B for
+ * every item), packed on the device per call. B items are [N,K] with row
+ * pitch ldb when trans_b (attention Q·Kᵀ), else [K,N] (P·V); b_dtype f32 or
+ * bf16. args->w must be NULL; every other field is as for ingot_rocm_gemm
+ * (f32 B runs f32 math unless math = INGOT_MATH_BF16). Replaces the
+ * per-batch-item loop of matmulOp for a batched right operand
+ * (ops/matmul.go:375-403). */
+int ingot_rocm_gemm_dynamic_b(ingot_rocm_session* s, const ingot_rocm_gemm_args* args, const void* d_b,
+                              int32_t b_dtype, int32_t trans_b, int64_t ldb, int64_t stride_b);
 
 /* Decode GEMV: y[m,n] = alpha·Σ_k x[m,k]·W[n,k] + beta·C (+act) for M <= 16
  * rows of f32 x against a bf16 weight, wavefront split-K with a deterministic

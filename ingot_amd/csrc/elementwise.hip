@@ -34,7 +34,13 @@ inline unsigned grid_for(int64_t work, int per_block) {
 // dst[j][k] (np × kp, dst_kind) = src element (j, k) of the logical [n][k]
 // weight, zero outside n × k. One thread per destination element.
 __global__ void pack_weight_kernel(const void* src, int src_dt, int64_t ld, int trans, int64_t n, int64_t k,
-                                   void* dst, int dst_kind, int64_t np, int64_t kp, int64_t ldk) {
+                                   void* dst, int dst_kind, int64_t np, int64_t kp, int64_t ldk, int64_t src_item,
+                                   int64_t dst_item) {
+    // blockIdx.y: matrix item (src_item / dst_item elements apart)
+    const int dsz = dst_kind == KIND_I8 ? 1 : (dst_kind == KIND_BF16 ? 2 : 4);
+    const int ssz = src_dt == INGOT_DT_F32 ? 4 : (src_dt == INGOT_DT_BF16 ? 2 : 1);
+    src = (const char*)src + blockIdx.y * src_item * ssz;
+    dst = (char*)dst + blockIdx.y * dst_item * dsz;
     const int64_t total = np * kp;
     for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
         const int64_t j = t / kp, kk = t - j * kp;
@@ -179,9 +185,10 @@ __global__ void fill_kernel(uint8_t* d, uint8_t v, size_t bytes) {
 }  // namespace
 
 hipError_t launch_pack_weight(const void* src, int src_dtype, int64_t ld, int trans, int64_t n, int64_t k, void* dst,
-                              GemmKind dst_kind, int64_t np, int64_t kp, int64_t ldk, hipStream_t st) {
-    hipLaunchKernelGGL(pack_weight_kernel, dim3(grid_for(np * kp, 256)), dim3(256), 0, st, src, src_dtype, ld, trans, n,
-                       k, dst, (int)dst_kind, np, kp, ldk);
+                              GemmKind dst_kind, int64_t np, int64_t kp, int64_t ldk, hipStream_t st, int items,
+                              int64_t src_item, int64_t dst_item) {
+    hipLaunchKernelGGL(pack_weight_kernel, dim3(grid_for(np * kp, 256), items), dim3(256), 0, st, src, src_dtype, ld,
+                       trans, n, k, dst, (int)dst_kind, np, kp, ldk, src_item, dst_item);
     return hipGetLastError();
 }
 

@@ -181,7 +181,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     // chunk (l%8) ^ (l/8), landing at LDS position l%8 of that row. Loads past
     // a buffer's end return zero (rows >= M; the weight is padded anyway).
     const __amdgpu_buffer_rsrc_t rsa = make_rsrc(p.a + (int64_t)blockIdx.y * p.stride_a_bytes, p.a_bytes);
-    const __amdgpu_buffer_rsrc_t rsb = make_rsrc(p.b, p.b_bytes);
+    const __amdgpu_buffer_rsrc_t rsb = make_rsrc(p.b + (int64_t)blockIdx.y * p.stride_b_bytes, p.b_bytes);
     // Lane l of a DMA covering rows R..R+7 (R a multiple of 8) writes position
     // l%8 of row R + l/8, so it fetches chunk (l%8) ^ swz(R + l/8); swz depends
     // on R only through bit 3 of R, giving two offsets per lane.

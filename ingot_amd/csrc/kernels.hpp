@@ -27,6 +27,7 @@ struct GemmArgs {
     int b_rows;          // allocated rows of b (loads clamp to it)
     int tiles_m, tiles_n;
     int64_t stride_a_bytes;  // per blockIdx.y batch item
+    int64_t stride_b_bytes;  // per blockIdx.y batch item (0: one weight for all)
     int64_t stride_y;        // elements, per batch item
     int a_xor;               // int8: flip the sign bit of A bytes (u8 → s8)
     int64_t a_plane_bytes;   // KIND_BF16X2: offset of the lo plane from the hi plane
@@ -76,8 +77,10 @@ hipError_t launch_pack_x(const float* x, int64_t ldx, int M, int K, int64_t kp, 
 // Packs a weight into [np][kp] of dst_kind, zero padded. src_dtype is an
 // INGOT_DT_* code; trans = 1: src is [n][k] (row pitch ld), 0: src is [k][n].
 // Rows of dst are ldk elements apart (ldk >= kp).
+// items > 1 packs that many matrices, src_item / dst_item elements apart.
 hipError_t launch_pack_weight(const void* src, int src_dtype, int64_t ld, int trans, int64_t n, int64_t k,
-                              void* dst, GemmKind dst_kind, int64_t np, int64_t kp, int64_t ldk, hipStream_t st);
+                              void* dst, GemmKind dst_kind, int64_t np, int64_t kp, int64_t ldk, hipStream_t st,
+                              int items = 1, int64_t src_item = 0, int64_t dst_item = 0);
 // colsum[j] = Σ_k packed[j][k] over an int8 packed weight (row pitch ldk).
 hipError_t launch_colsum_i8(const int8_t* packed, int64_t kp, int64_t ldk, int64_t n, int32_t* colsum,
                             hipStream_t st);

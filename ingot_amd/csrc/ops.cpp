@@ -533,29 +533,53 @@ class MatMulOp : public Op {
                 rc = ingot_rocm_gemm(s, &g);
                 if (rc) return n.errorf(rc, "%s", ingot_rocm_last_error());
             } else {
-                // per-batch products with broadcast operand offsets (ops/matmul.go:375-403)
+                // Batched right operand (attention Q·Kᵀ / P·V): per-batch products
+                // with broadcast operand offsets (ops/matmul.go:375-403). B is an
+                // activation, packed on the device per call; when both operands'
+                // matrix offsets are linear in the output batch index (equal batch
+                // shapes, or one side broadcast whole) all items run as one
+                // batched launch, otherwise one call per item.
                 const auto sa = broadcast_strides(batchA, batch);
                 const auto sb = broadcast_strides(batchB, batch);
-                std::vector<int64_t> idx(batch.size(), 0);
-                TempWeights tmp(s);
+                std::vector<int64_t> offA((size_t)nb), offB((size_t)nb), idx(batch.size(), 0);
                 for (int64_t bi = 0; bi < nb; ++bi) {
-                    int64_t offA = 0, offB = 0;
+                    int64_t oa = 0, ob = 0;
                     for (size_t d = 0; d < idx.size(); ++d) {
-                        offA += idx[d] * sa[d];
-                        offB += idx[d] * sb[d];
+                        oa += idx[d] * sa[d];
+                        ob += idx[d] * sb[d];
                     }
-                    ingot_rocm_weight* w = nullptr;
-                    rc = tmp.pack(INGOT_DT_F32, pack_dt, K, N, 0, (const float*)b.data + offB * K * N, &w);
-                    if (rc) return rc;
-                    g.M = M;
-                    g.d_a = (const float*)a.data + offA * M * K;
-                    g.w = w;
-                    g.d_y = (float*)out.data + bi * M * N;
-                    rc = ingot_rocm_gemm(s, &g);
-                    if (rc) return n.errorf(rc, "%s", ingot_rocm_last_error());
+                    offA[(size_t)bi] = oa;
+                    offB[(size_t)bi] = ob;
                     for (int64_t d = (int64_t)idx.size() - 1; d >= 0; --d) {
-                        if (++idx[d] < batch[d]) break;
-                        idx[d] = 0;
+                        if (++idx[(size_t)d] < batch[(size_t)d]) break;
+                        idx[(size_t)d] = 0;
+                    }
+                }
+                const int64_t cA = nb > 1 ? offA[1] - offA[0] : 0, cB = nb > 1 ? offB[1] - offB[0] : 0;
+                bool linear = offA[0] == 0 && offB[0] == 0;
+                for (int64_t bi = 0; bi < nb && linear; ++bi)
+                    linear = offA[(size_t)bi] == bi * cA && offB[(size_t)bi] == bi * cB;
+                g.M = M;
+                const float* A = (const float*)a.data;
+                const float* B = (const float*)b.data;
+                float* Y = (float*)out.data;
+                if (linear) {
+                    for (int64_t b0 = 0; b0 < nb; b0 += 65535) {
+                        g.batch = std::min<int64_t>(65535, nb - b0);
+                        g.d_a = A + b0 * cA * M * K;
+                        g.stride_a = cA * M * K;
+                        g.d_y = Y + b0 * M * N;
+                        g.stride_y = M * N;
+                        rc = ingot_rocm_gemm_dynamic_b(s, &g, B + b0 * cB * K * N, INGOT_DT_F32, 0, N, cB * K * N);
+                        if (rc) return n.errorf(rc, "%s", ingot_rocm_last_error());
+                    }
+                } else {
+                    g.batch = 1;
+                    for (int64_t bi = 0; bi < nb; ++bi) {
+                        g.d_a = A + offA[(size_t)bi] * M * K;
+                        g.d_y = Y + bi * M * N;
+                        rc = ingot_rocm_gemm_dynamic_b(s, &g, B + offB[(size_t)bi] * K * N, INGOT_DT_F32, 0, N, 0);
+                        if (rc) return n.errorf(rc, "%s", ingot_rocm_last_error());
                     }
                 }
             }

@@ -409,8 +409,7 @@ int ingot_rocm_weight_info(const ingot_rocm_weight* w, int64_t* n, int64_t* k, i
 
 // ---------------- GEMM / GEMV ----------------
 
-static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
-    const ingot_rocm_weight* w = a->w;
+static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w) {
     GemvArgs g;
     memset(&g, 0, sizeof g);
     g.x = (const float*)a->d_a;
@@ -444,11 +443,10 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     return INGOT_OK;
 }
 
-static int validate_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
+static int validate_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w) {
     int rc = session_enter(s);
     if (rc) return rc;
-    if (!a || !a->w) return fail(INGOT_EINVAL, "gemm: nil arguments or weight");
-    const ingot_rocm_weight* w = a->w;
+    if (!a || !w) return fail(INGOT_EINVAL, "gemm: nil arguments or weight");
     if (a->M < 0 || a->N != w->n || a->K != w->k)
         return fail(INGOT_EINVAL, "gemm: shape M=%lld N=%lld K=%lld does not match weight [%lld,%lld]", (long long)a->M,
                     (long long)a->N, (long long)a->K, (long long)w->n, (long long)w->k);
@@ -459,6 +457,7 @@ static int validate_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     if (a->lda < amin) return fail(INGOT_EINVAL, "gemm: lda %lld < %lld", (long long)a->lda, (long long)amin);
     if (a->ldy < a->N) return fail(INGOT_EINVAL, "gemm: ldy %lld < N %lld", (long long)a->ldy, (long long)a->N);
     if (a->M > INT32_MAX / 2 || a->N > INT32_MAX / 2) return fail(INGOT_EINVAL, "gemm: dimension too large");
+    if (a->batch > 65535) return fail(INGOT_EINVAL, "gemm: batch %lld > 65535", (long long)a->batch);
     if (a->math == INGOT_MATH_F32 && w->kind != KIND_F32)
         return fail(INGOT_EDECLINED, "gemm: f32 math needs an f32-packed weight");
     if (a->math == INGOT_MATH_BF16 && w->kind != KIND_BF16)
@@ -469,23 +468,24 @@ static int validate_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
 }
 
 int ingot_rocm_gemv_bf16(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
-    int rc = validate_gemm(s, a);
+    int rc = validate_gemm(s, a, a ? a->w : nullptr);
     if (rc) return rc;
     if (a->w->kind != KIND_BF16 || a->M > 16 || a->a_dtype != INGOT_DT_F32 || a->trans_a || a->batch > 1)
         return fail(INGOT_EINVAL, "gemv_bf16: needs M <= 16 rows of f32 A (no transA, no batch) and a bf16 weight");
     if (a->M == 0) return INGOT_OK;
-    return run_gemv(s, a);
+    return run_gemv(s, a, a->w);
 }
 
-int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
-    int rc = validate_gemm(s, a);
-    if (rc) return rc;
-    const ingot_rocm_weight* w = a->w;
+// The GEMM after validation. w may be a session weight or a per-call packed
+// operand; stride_b_bytes advances it per batch item (0: shared).
+static int gemm_core(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w,
+                     int64_t stride_b_bytes) {
+    int rc;
     const int64_t batch = std::max<int64_t>(1, a->batch);
     if (a->M == 0 || a->N == 0) return INGOT_OK;
     if (w->kind == KIND_BF16 && a->M <= 16 && !a->trans_a && a->a_dtype == INGOT_DT_F32 && batch == 1 &&
         !getenv("INGOT_NO_GEMV"))
-        return run_gemv(s, a);
+        return run_gemv(s, a, w);
 
     // bf16 weights with f32 activations: two bf16 planes (f32-class accuracy)
     // unless the caller asked for single bf16 rounding (INGOT_MATH_BF16).
@@ -530,6 +530,7 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     }
     g.b = (const char*)w->data;
     g.ldb_bytes = w->ldk * esz;
+    g.stride_b_bytes = stride_b_bytes;
     g.M = (int)a->M;
     g.N = (int)a->N;
     g.kt = (int)(kl * esz / KTILE_BYTES);
@@ -546,6 +547,57 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     hipError_t e = launch_gemm(kind, cfg, g, (int)batch, s->stream);
     if (e != hipSuccess) return hip_fail(e, "gemm launch");
     return INGOT_OK;
+}
+
+int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
+    int rc = validate_gemm(s, a, a ? a->w : nullptr);
+    if (rc) return rc;
+    return gemm_core(s, a, a->w, 0);
+}
+
+int ingot_rocm_gemm_dynamic_b(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const void* d_b, int32_t b_dtype,
+                              int32_t trans_b, int64_t ldb, int64_t stride_b) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!a) return fail(INGOT_EINVAL, "gemm_dynamic_b: nil arguments");
+    if (a->w) return fail(INGOT_EINVAL, "gemm_dynamic_b: B comes from d_b; the weight handle must be NULL");
+    if (b_dtype != INGOT_DT_F32 && b_dtype != INGOT_DT_BF16)
+        return fail(INGOT_EINVAL, "gemm_dynamic_b: B must be f32 or bf16");
+    if (a->M < 0 || a->N < 0 || a->K < 0 || stride_b < 0)
+        return fail(INGOT_EINVAL, "gemm_dynamic_b: negative size or stride");
+    if (a->N > 0 && a->K > 0 && ldb < (trans_b ? a->K : a->N))
+        return fail(INGOT_EINVAL, "gemm_dynamic_b: ldb %lld < %lld", (long long)ldb, (long long)(trans_b ? a->K : a->N));
+    if (a->M == 0 || a->N == 0) return INGOT_OK;
+    if (a->K == 0) return fail(INGOT_EDECLINED, "gemm_dynamic_b: K = 0");
+    if (!d_b) return fail(INGOT_EINVAL, "gemm_dynamic_b: nil B");
+    // f32 B packs as f32 (exact) unless bf16 math was asked for; bf16 B packs
+    // as bf16 unless f32 math was asked for (exact widening).
+    const bool f32 = a->math == INGOT_MATH_F32 || (b_dtype == INGOT_DT_F32 && a->math != INGOT_MATH_BF16);
+    ingot_rocm_weight wt;
+    memset(&wt, 0, sizeof wt);
+    wt.kind = f32 ? KIND_F32 : KIND_BF16;
+    wt.pack_dtype = f32 ? INGOT_DT_F32 : INGOT_DT_BF16;
+    wt.n = a->N;
+    wt.k = a->K;
+    wt.np = round_up(a->N, 256);
+    wt.kp = round_up(a->K, 256);
+    wt.ldk = wt.kp + 128 / kind_size(wt.kind);
+    const int64_t batch = std::max<int64_t>(1, a->batch);
+    const int items = stride_b ? (int)batch : 1;
+    const int64_t item = wt.np * wt.ldk;
+    rc = validate_gemm(s, a, &wt);
+    if (rc) return rc;
+    wt.data = pool_get(s, (size_t)(items * item * kind_size(wt.kind)));
+    if (!wt.data) return fail(INGOT_ENOMEM, "gemm_dynamic_b: cannot allocate the packed B");
+    hipError_t e = launch_pack_weight(d_b, b_dtype, ldb, trans_b ? 1 : 0, a->N, a->K, wt.data, wt.kind, wt.np, wt.kp,
+                                      wt.ldk, s->stream, items, stride_b, item);
+    if (e != hipSuccess) {
+        pool_put(s, wt.data);
+        return hip_fail(e, "pack B");
+    }
+    rc = gemm_core(s, a, &wt, stride_b ? item * kind_size(wt.kind) : 0);
+    pool_put(s, wt.data);  // stream-ordered: later users of the buffer queue behind this GEMM
+    return rc;
 }
 
 int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64_t K, const void* d_a, int32_t a_dtype,

@@ -179,29 +179,38 @@ class Session:
         return Weight(self, h.value)
 
     # ---- kernel layer ----
-    def gemm_args(self, a: DeviceTensor, w: Weight, y: DeviceTensor, M: int, **kw) -> L.GemmArgs:
+    def gemm_args(self, a: DeviceTensor, w: Optional[Weight], y: DeviceTensor, M: int, **kw) -> L.GemmArgs:
+        """Argument block; without a weight, N and K come from kw["n"], kw["k"]."""
         g = L.GemmArgs()
-        g.M, g.N, g.K = M, w.n, w.k
+        n, k = (w.n, w.k) if w is not None else (kw["n"], kw["k"])
+        g.M, g.N, g.K = M, n, k
         g.d_a, g.a_dtype = a.ptr, kw.get("a_dtype", a.dtype)
         g.trans_a = 1 if kw.get("trans_a") else 0
-        g.lda = kw.get("lda", M if g.trans_a else w.k)
-        g.w = w.h
+        g.lda = kw.get("lda", M if g.trans_a else k)
+        g.w = w.h if w is not None else None
         g.alpha, g.beta = kw.get("alpha", 1.0), kw.get("beta", 0.0)
         c = kw.get("c")
         g.d_c = c.ptr if c is not None else None
         g.c_mode = kw.get("c_mode", L.C_NONE)
         g.math = kw.get("math", L.MATH_AUTO)
-        g.ldc = kw.get("ldc", w.n)
+        g.ldc = kw.get("ldc", n)
         g.act, g.act_alpha, g.act_beta = kw.get("act", L.ACT_NONE), kw.get("act_alpha", 0.0), kw.get("act_beta", 0.0)
         g.post = 1 if kw.get("post") else 0
         g.post_scale, g.post_shift = kw.get("post_scale", 1.0), kw.get("post_shift", 0.0)
-        g.d_y, g.ldy = y.ptr, kw.get("ldy", w.n)
+        g.d_y, g.ldy = y.ptr, kw.get("ldy", n)
         g.batch, g.stride_a, g.stride_y = kw.get("batch", 1), kw.get("stride_a", 0), kw.get("stride_y", 0)
         return g
 
     def gemm(self, a: DeviceTensor, w: Weight, y: DeviceTensor, M: int, **kw) -> None:
         g = self.gemm_args(a, w, y, M, **kw)
         L.check(self.lib.ingot_rocm_gemm(self.h, C.byref(g)))
+
+    def gemm_dynamic_b(self, a: DeviceTensor, b: DeviceTensor, y: DeviceTensor, M: int, N: int, K: int,
+                       trans_b: bool, ldb: int, stride_b: int, **kw) -> None:
+        """Batched GEMM with a per-item activation B (ingot_rocm_gemm_dynamic_b)."""
+        g = self.gemm_args(a, None, y, M, n=N, k=K, **kw)
+        L.check(self.lib.ingot_rocm_gemm_dynamic_b(self.h, C.byref(g), b.ptr, b.dtype, 1 if trans_b else 0, ldb,
+                                                   stride_b))
 
     def gemv_bf16(self, a: DeviceTensor, w: Weight, y: DeviceTensor, M: int, **kw) -> None:
         g = self.gemm_args(a, w, y, M, **kw)

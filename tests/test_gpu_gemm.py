@@ -153,6 +153,47 @@ def test_gemm_batched_strided(sess):
         assert_close(got[i], oracle.gemm(a[i], bt, trans_b=True), nstar_tol(k, a, bt), f"batch {i}")
 
 
+@pytest.mark.parametrize("trans_b", [1, 0])
+@pytest.mark.parametrize("b_dt", ["f32", "bf16"])
+@pytest.mark.parametrize("shared", [False, True])
+def test_gemm_dynamic_b(sess, trans_b, b_dt, shared):
+    """Per-item activation B (ingot_rocm_gemm_dynamic_b): Q·Kᵀ (B items [N,K]) and P·V (B items [K,N])."""
+    announce(f"gemm dynamic b trans_b={trans_b} {b_dt} shared={shared}")
+    rng = np.random.default_rng(3 + trans_b + 2 * shared)
+    bsz, m, n, k, ldb_pad = 5, 70, 50, 37, 3
+    a = rng.uniform(-1, 1, (bsz, m, k)).astype(np.float32)
+    items = 1 if shared else bsz
+    rows, cols = (n, k) if trans_b else (k, n)
+    if b_dt == "bf16":
+        bb = bf16_weights(rng, (items, rows, cols + ldb_pad), 1.0, "uniform")
+        bw = oracle.bf16_to_f32(bb)
+        db = sess.to_device(bb, L.DT_BF16)
+    else:
+        bw = rng.uniform(-1, 1, (items, rows, cols + ldb_pad)).astype(np.float32)
+        db = sess.to_device(bw)
+    y = sess.empty(L.DT_F32, (bsz, m, n))
+    sess.gemm_dynamic_b(sess.to_device(a), db, y, m, n, k, bool(trans_b), cols + ldb_pad,
+                        0 if shared else rows * (cols + ldb_pad), batch=bsz, stride_a=m * k, stride_y=m * n)
+    got = y.numpy()
+    for i in range(bsz):
+        bi = bw[0 if shared else i][:, :cols]
+        want = oracle.gemm(a[i], np.ascontiguousarray(bi), trans_b=bool(trans_b))
+        assert_close(got[i], want, nstar_tol(k, a, bi), f"dynamic b item {i}")
+
+
+def test_gemm_dynamic_b_decode_route(sess):
+    """M <= 16, one item, bf16 B: the per-call packed B takes the GEMV route."""
+    announce("gemm dynamic b gemv route")
+    rng = np.random.default_rng(21)
+    m, n, k = 9, 300, 640
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    y = sess.empty(L.DT_F32, (m, n))
+    sess.gemm_dynamic_b(sess.to_device(x), sess.to_device(wb, L.DT_BF16), y, m, n, k, True, k, 0)
+    want = oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16)
+    assert_close(y.numpy(), want, nstar_tol(k, x, oracle.bf16_to_f32(wb)), "dynamic b gemv")
+
+
 @pytest.mark.parametrize("m", [1, 2, 4, 7, 16])
 @pytest.mark.parametrize("n,k", [(64, 256), (200, 300), (2048, 2048), (1000, 5632)])
 def test_gemv_bf16_decode(sess, m, n, k):

@@ -80,6 +80,26 @@ def test_matmul_broadcast_batch(sess, as_, bs):
     assert_close(y, want, nstar_tol(bs[0], a, b), "matmul bcast")
 
 
+@pytest.mark.parametrize("as_,bs", [((2, 3, 77, 40), (2, 3, 40, 77)), ((2, 3, 77, 77), (2, 3, 77, 40)),
+                                    ((96, 128, 64), (96, 64, 128)), ((2, 1, 9, 16), (1, 3, 16, 11)),
+                                    ((9, 16), (4, 16, 11)), ((4, 9, 16), (1, 16, 11)), ((3, 1, 5), (3, 5, 1))])
+def test_matmul_batched_rhs(sess, as_, bs):
+    """Batched right operand (attention Q·Kᵀ and P·V shapes, ops/matmul.go:375-403): equal batch shapes,
+    whole-side broadcast and a mixed broadcast that needs per-item products; run 2 bit-identical."""
+    announce(f"op matmul batched rhs {as_} {bs}")
+    rng = np.random.default_rng(17)
+    a = rng.uniform(-1, 1, as_).astype(np.float32)
+    b = rng.uniform(-1, 1, bs).astype(np.float32)
+    op = sess.op("MatMul", 13)
+    da, db = dev(sess, a), dev(sess, b)
+    (y,) = run(op, da, db)
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64))
+    assert y.shape == want.shape
+    assert_close(y, want, nstar_tol(bs[-2], a, b), "matmul batched rhs")
+    (y2,) = run(op, da, db)
+    assert np.array_equal(y, y2), "second run differs"
+
+
 @pytest.mark.parametrize("as_,bs", [((128, 384), (384, 1152)), ((1, 16, 48), (48, 144)), ((7, 1, 384), (384, 96)),
                                     ((5, 13), (13, 7)), ((2, 3, 4, 33), (33, 5)), ((2, 8, 32), (2, 32, 96))])
 def test_matmul_bias(sess, as_, bs):
