@@ -233,6 +233,17 @@ int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64
                               int32_t a_dtype, int64_t lda, int32_t za, const ingot_rocm_weight* w, int32_t* d_y_i32,
                               const float* d_dq_scale, int64_t n_scale, int32_t dq_zp, float* d_y_f32);
 
+/* QLinearMatMul (ops/quant.go:791-928, requant branch): the product of
+ * ingot_rocm_matmul_integer requantised on the device,
+ *   Y[m,n] = sat(RoundToEven(fl32(fl32(float32(Y_i32[m,n])·mult) + zy))),
+ * saturated to [0,255] (y_dtype INGOT_DT_U8, satU8 ops/quant.go:26-35) or
+ * [-128,127] (INGOT_DT_I8, satI8 :37-46). mult = fl32(fl32(a_scale·b_scale)
+ * / y_scale) is computed by the caller as the reference does (per-tensor
+ * scales, :911). The multiply and the add are rounded separately. */
+int ingot_rocm_qlinear_matmul(ingot_rocm_session* s, int64_t M, int64_t N, int64_t K, const void* d_a,
+                              int32_t a_dtype, int64_t lda, int32_t za, const ingot_rocm_weight* w, float mult,
+                              int32_t zy, int32_t y_dtype, void* d_y);
+
 /* DequantizeLinear over a dense tensor of n elements (ops/quant.go:173-229):
  *   y[i] = float32(x[i] − zp[c]) · scale[c],  c = (i / inner) % n_scale
  * x_dtype U8, I8 or I32; n_scale 1 = per-tensor (then inner is ignored);

@@ -72,6 +72,9 @@ SIGNATURES = {
     "ingot_rocm_gemm_dynamic_b": (C.c_int, [C.c_void_p, C.POINTER(GemmArgs), C.c_void_p, C.c_int32, C.c_int32,
                                             C.c_int64, C.c_int64]),
     "ingot_rocm_gemv_bf16": (C.c_int, [C.c_void_p, C.POINTER(GemmArgs)]),
+    "ingot_rocm_qlinear_matmul": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_int32,
+                                            C.c_int64, C.c_int32, C.c_void_p, C.c_float, C.c_int32, C.c_int32,
+                                            C.c_void_p]),
     "ingot_rocm_matmul_integer": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_int32,
                                             C.c_int64, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                             C.c_int32, C.c_void_p]),

@@ -110,6 +110,10 @@ struct QEpi {
     const float* scale;
     int64_t n_scale;
     int32_t dq_zp;
+    // QLinearMatMul (ops/quant.go:902-928): yq = sat(rne(fl32(fl32(float(yi))·rq_mult) + rq_zy))
+    void* yq;
+    int yq_u8;  // 1: u8 [0,255]; 0: s8 [-128,127]
+    float rq_mult, rq_zy;
 };
 
 __device__ __forceinline__ int32_t wrap_mul(int32_t a, int32_t b) {

@@ -319,7 +319,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     // 16-byte stores need an aligned row start (n is always a multiple of 4 here)
     uintptr_t ybase;
     if (KD == KIND_I8)
-        ybase = (uintptr_t)(p.qepi.yi ? p.qepi.yi + ybatch : nullptr) | (uintptr_t)(p.qepi.yf ? p.qepi.yf + ybatch : nullptr);
+        ybase = (uintptr_t)(p.qepi.yi ? p.qepi.yi + ybatch : nullptr) | (uintptr_t)(p.qepi.yf ? p.qepi.yf + ybatch : nullptr) |
+                (uintptr_t)(p.qepi.yq ? (uint8_t*)p.qepi.yq + ybatch : nullptr);
     else
         ybase = (uintptr_t)((float*)p.y + ybatch);
     const bool vec_ok = (ybase & 15) == 0 && (p.ldy & 3) == 0;
@@ -358,6 +359,28 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
                     for (int e = 0; e < 4 && n + e < p.N; ++e) {
                         if (q.yi) q.yi[o + e] = v[e];
                         if (q.yf) q.yf[o + e] = f[e];
+                    }
+                }
+                if (q.yq) {
+                    // the product and the sum rounded separately (no contraction into
+                    // an FMA), then half-to-even and saturation
+#pragma clang fp contract(off)
+                    uint32_t packed = 0;
+                    uint8_t qb[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float t = (float)v[e] * q.rq_mult;
+                        const float r = rintf(t + q.rq_zy);
+                        const int iv = q.yq_u8 ? (r <= 0.f ? 0 : (r >= 255.f ? 255 : (int)r))
+                                               : (r <= -128.f ? -128 : (r >= 127.f ? 127 : (int)r));
+                        qb[e] = (uint8_t)iv;
+                        packed |= (uint32_t)qb[e] << (8 * e);
+                    }
+                    uint8_t* yq = (uint8_t*)q.yq;
+                    if (full && vec_ok) {
+                        *(uint32_t*)(yq + o) = packed;
+                    } else {
+                        for (int e = 0; e < 4 && n + e < p.N; ++e) yq[o + e] = qb[e];
                     }
                 }
             }

@@ -6,7 +6,7 @@
 // so a caller sees the same failures (NodeInfo.Errorf: "Op(name): msg").
 //
 // Ops: Gemm@7 and MatMul@1 (ops/matmul.go:27-139, 305-438, 454-472),
-// MatMulInteger@10 (ops/quant.go:791-900, 943), DequantizeLinear@10
+// MatMulInteger@10 and QLinearMatMul@10 (ops/quant.go:791-928, 942-943), DequantizeLinear@10
 // (ops/quant.go:168-230, 947-949), and the activation nodes a GEMM epilogue
 // can absorb: Relu@6, Sigmoid@6, HardSwish@14, LeakyRelu@6, HardSigmoid@6,
 // Gelu@20, ingot.Gelu@1, ingot.SiLU@1 (ops/elementwise.go:486-545).
@@ -254,6 +254,12 @@ int read_ints(ingot_rocm_session* s, const T& t, std::vector<int32_t>* out) {
         }
     }
     return INGOT_OK;
+}
+
+// First element of an f32 tensor (per-tensor quantisation scales).
+int read_f32_first(ingot_rocm_session* s, const T& t, float* out) {
+    if (t.dtype != INGOT_DT_F32 || t.n() < 1) return fail(INGOT_EINVAL, "scale must be a non-empty f32 tensor");
+    return ingot_rocm_memcpy_d2h(s, out, t.data, sizeof(float));
 }
 
 // bCache (ops/matmul.go:200-236): the packed form of a B that is the same
@@ -597,10 +603,12 @@ class MatMulOp : public Op {
 
 // ---------------- MatMulInteger ----------------
 
-// qmatmulOp with requant=false (ops/quant.go:791-900).
+// qmatmulOp (ops/quant.go:791-928): MatMulInteger (requant = false, int32
+// out) and QLinearMatMul (requant = true, u8/s8 out).
 class MatMulIntegerOp : public Op {
    public:
     NodeInfo n;
+    bool requant = false;
     ingot_rocm_session* s;
     std::mutex mu;
     const void* pack_src = nullptr;
@@ -647,11 +655,20 @@ class MatMulIntegerOp : public Op {
     }
 
     int run(Ctx& ctx, const std::vector<T>& in) override {
-        if (in.size() < 2) return n.errorf(INGOT_EINVAL, "need 2-4 inputs");
-        const T& a = in[0];
-        const T& b = in[1];
-        const T* aZp = in.size() > 2 && in[2].present() ? &in[2] : nullptr;
-        const T* bZp = in.size() > 3 && in[3].present() ? &in[3] : nullptr;
+        auto opt = [&](size_t i) { return in.size() > i && in[i].present() ? &in[i] : nullptr; };
+        const T *pa, *pb, *aZp, *bZp, *aScale = nullptr, *bScale = nullptr, *yScale = nullptr, *yZp = nullptr;
+        if (requant) {
+            if (in.size() < 8 || !in[0].present() || !in[1].present() || !in[3].present() || !in[4].present() ||
+                !in[6].present())
+                return n.errorf(INGOT_EINVAL, "need 8 inputs");
+            pa = &in[0], aScale = &in[1], aZp = opt(2), pb = &in[3], bScale = &in[4], bZp = opt(5), yScale = &in[6],
+            yZp = opt(7);
+        } else {
+            if (in.size() < 2 || !in[0].present() || !in[1].present()) return n.errorf(INGOT_EINVAL, "need 2-4 inputs");
+            pa = &in[0], pb = &in[1], aZp = opt(2), bZp = opt(3);
+        }
+        const T& a = *pa;
+        const T& b = *pb;
         int rc = s8_weights(b, bZp);
         if (rc) return rc;
         if (a.rank() != 2 || b.rank() != 2 || a.dim(1) != b.dim(0))
@@ -670,19 +687,51 @@ class MatMulIntegerOp : public Op {
         }
         if (a.dtype != INGOT_DT_U8 && a.dtype != INGOT_DT_I8)
             return n.errorf(INGOT_EINVAL, "activations must be u8 or s8, got %s", dtype_name(a.dtype));
+        // QLinearMatMul: per-tensor scales (element 0, ops/quant.go:911) and the
+        // output zero point, whose dtype is the output dtype (quantParams,
+        // ops/quant.go:50-72; absent: u8, 0)
+        float mult = 0.f;
+        int32_t zy = 0;
+        int ydt = INGOT_DT_I32;
+        if (requant) {
+            float sa, sb, sy;
+            if ((rc = read_f32_first(s, *aScale, &sa)) || (rc = read_f32_first(s, *bScale, &sb)) ||
+                (rc = read_f32_first(s, *yScale, &sy)))
+                return n.errorf(rc, "%s", ingot_rocm_last_error());
+            volatile float ab = sa * sb;
+            mult = ab / sy;
+            ydt = INGOT_DT_U8;
+            if (yZp) {
+                std::vector<int32_t> z;
+                if (yZp->dtype != INGOT_DT_U8 && yZp->dtype != INGOT_DT_I8)
+                    return n.errorf(INGOT_EINVAL, "unsupported output quantization");
+                rc = read_ints(s, *yZp, &z);
+                if (rc) return rc;
+                if (z.size() != 1) return n.errorf(INGOT_EINVAL, "unsupported output quantization");
+                ydt = yZp->dtype;
+                zy = z[0];
+            }
+        }
         T out;
-        rc = ctx.new_uninit(INGOT_DT_I32, {m, nn}, &out);
+        rc = ctx.new_uninit(ydt, {m, nn}, &out);
         if (rc) return rc;
         if (m > 0 && nn > 0) {
             if (k == 0) {
-                rc = ingot_rocm_memset(s, out.data, 0, (size_t)(m * nn * 4));
+                // empty reduction: every product is 0, so Y = sat(zy) (or 0 for int32 out)
+                const int fill = !requant ? 0 : ydt == INGOT_DT_U8 ? std::min(255, std::max(0, zy))
+                                                                   : std::min(127, std::max(-128, zy));
+                rc = ingot_rocm_memset(s, out.data, fill & 0xFF,
+                                       (size_t)(m * nn * (requant ? 1 : 4)));
                 if (rc) return rc;
             } else {
                 ingot_rocm_weight* w = nullptr;
                 rc = b_weights(b, k, nn, &w);
                 if (rc) return rc;
-                rc = ingot_rocm_matmul_integer(s, m, nn, k, a.data, a.dtype, k, za, w, (int32_t*)out.data, nullptr, 1,
-                                               0, nullptr);
+                if (requant)
+                    rc = ingot_rocm_qlinear_matmul(s, m, nn, k, a.data, a.dtype, k, za, w, mult, zy, ydt, out.data);
+                else
+                    rc = ingot_rocm_matmul_integer(s, m, nn, k, a.data, a.dtype, k, za, w, (int32_t*)out.data,
+                                                   nullptr, 1, 0, nullptr);
                 if (rc) return n.errorf(rc, "%s", ingot_rocm_last_error());
             }
         }
@@ -790,6 +839,14 @@ void register_all() {
         Register("", "MatMulInteger", 10, [](const NodeInfo& n, std::unique_ptr<Op>* out) {
             auto op = std::make_unique<MatMulIntegerOp>();
             op->n = n;
+            op->s = t_build_session;
+            *out = std::move(op);
+            return INGOT_OK;
+        });
+        Register("", "QLinearMatMul", 10, [](const NodeInfo& n, std::unique_ptr<Op>* out) {
+            auto op = std::make_unique<MatMulIntegerOp>();
+            op->n = n;
+            op->requant = true;
             op->s = t_build_session;
             *out = std::move(op);
             return INGOT_OK;

@@ -600,9 +600,11 @@ int ingot_rocm_gemm_dynamic_b(ingot_rocm_session* s, const ingot_rocm_gemm_args*
     return rc;
 }
 
-int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64_t K, const void* d_a, int32_t a_dtype,
-                              int64_t lda, int32_t za, const ingot_rocm_weight* w, int32_t* d_y_i32,
-                              const float* d_dq_scale, int64_t n_scale, int32_t dq_zp, float* d_y_f32) {
+// The int8 GEMM with its outputs: int32 (yi), dequantised f32 (yf) and/or
+// requantised u8/s8 (yq).
+static int qgemm(ingot_rocm_session* s, int64_t M, int64_t N, int64_t K, const void* d_a, int32_t a_dtype, int64_t lda,
+                 int32_t za, const ingot_rocm_weight* w, int32_t* d_y_i32, const float* d_dq_scale, int64_t n_scale,
+                 int32_t dq_zp, float* d_y_f32, void* d_yq, int yq_u8, float rq_mult, float rq_zy) {
     int rc = session_enter(s);
     if (rc) return rc;
     if (!w || w->kind != KIND_I8) return fail(INGOT_EINVAL, "matmul_integer: weight must be packed as int8");
@@ -610,7 +612,7 @@ int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64
         return fail(INGOT_EINVAL, "matmul_integer: shape M=%lld N=%lld K=%lld does not match weight [%lld,%lld]",
                     (long long)M, (long long)N, (long long)K, (long long)w->n, (long long)w->k);
     if (a_dtype != INGOT_DT_U8 && a_dtype != INGOT_DT_I8) return fail(INGOT_EINVAL, "matmul_integer: A must be u8 or s8");
-    if (!d_y_i32 && !d_y_f32) return fail(INGOT_EINVAL, "matmul_integer: no output");
+    if (!d_y_i32 && !d_y_f32 && !d_yq) return fail(INGOT_EINVAL, "matmul_integer: no output");
     if (d_y_f32 && (!d_dq_scale || (n_scale != 1 && n_scale != N)))
         return fail(INGOT_EINVAL, "matmul_integer: dequant scale must have 1 or N elements");
     if (lda < K) return fail(INGOT_EINVAL, "matmul_integer: lda < K");
@@ -655,6 +657,10 @@ int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64
     g.qepi.scale = d_dq_scale;
     g.qepi.n_scale = n_scale;
     g.qepi.dq_zp = dq_zp;
+    g.qepi.yq = d_yq;
+    g.qepi.yq_u8 = yq_u8;
+    g.qepi.rq_mult = rq_mult;
+    g.qepi.rq_zy = rq_zy;
     const int cfg = pick_config(KIND_I8, M, N, 1, s->num_cus);
     const GemmConfig* c;
     gemm_configs(KIND_I8, &c);
@@ -663,6 +669,23 @@ int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64
     hipError_t e = launch_gemm(KIND_I8, cfg, g, 1, s->stream);
     if (e != hipSuccess) return hip_fail(e, "qgemm launch");
     return INGOT_OK;
+}
+
+int ingot_rocm_matmul_integer(ingot_rocm_session* s, int64_t M, int64_t N, int64_t K, const void* d_a, int32_t a_dtype,
+                              int64_t lda, int32_t za, const ingot_rocm_weight* w, int32_t* d_y_i32,
+                              const float* d_dq_scale, int64_t n_scale, int32_t dq_zp, float* d_y_f32) {
+    return qgemm(s, M, N, K, d_a, a_dtype, lda, za, w, d_y_i32, d_dq_scale, n_scale, dq_zp, d_y_f32, nullptr, 0, 0.f,
+                 0.f);
+}
+
+int ingot_rocm_qlinear_matmul(ingot_rocm_session* s, int64_t M, int64_t N, int64_t K, const void* d_a, int32_t a_dtype,
+                              int64_t lda, int32_t za, const ingot_rocm_weight* w, float mult, int32_t zy,
+                              int32_t y_dtype, void* d_y) {
+    if (y_dtype != INGOT_DT_U8 && y_dtype != INGOT_DT_I8)
+        return fail(INGOT_EINVAL, "qlinear_matmul: output must be u8 or s8");
+    if (!d_y && M > 0 && N > 0) return fail(INGOT_EINVAL, "qlinear_matmul: nil Y");
+    return qgemm(s, M, N, K, d_a, a_dtype, lda, za, w, nullptr, nullptr, 1, 0, nullptr, d_y,
+                 y_dtype == INGOT_DT_U8 ? 1 : 0, mult, (float)zy);
 }
 
 int ingot_rocm_dequantize_linear(ingot_rocm_session* s, const void* d_x, int32_t x_dtype, int64_t n,

@@ -224,6 +224,12 @@ class Session:
             y_i32.ptr if y_i32 is not None else None, scale.ptr if scale is not None else None,
             scale.numel if scale is not None else 1, dq_zp, y_f32.ptr if y_f32 is not None else None))
 
+    def qlinear_matmul(self, a: DeviceTensor, w: Weight, M: int, za: int, mult: float, zy: int, y: DeviceTensor,
+                       lda: Optional[int] = None) -> None:
+        """QLinearMatMul product requantised to y's dtype (u8 or s8)."""
+        L.check(self.lib.ingot_rocm_qlinear_matmul(
+            self.h, M, w.n, w.k, a.ptr, a.dtype, lda if lda is not None else w.k, za, w.h, mult, zy, y.dtype, y.ptr))
+
     def dequantize_linear(self, x: DeviceTensor, scale: DeviceTensor, y: DeviceTensor, inner: int = 1,
                           zp: Optional[DeviceTensor] = None) -> None:
         L.check(self.lib.ingot_rocm_dequantize_linear(

@@ -56,6 +56,9 @@ def lib() -> C.CDLL:
         L.orc_matmul_integer.argtypes = [_I64, _I64, _I64, _P, C.c_int, C.c_int32, _P, _P]
         L.orc_matmul_integer_shifted.argtypes = [_I64, _I64, _I64, _P, C.c_int, C.c_int32, _P, _P]
         L.orc_dequantize_linear.argtypes = [_P, C.c_int, _I64, _P, _I64, _I64, _P, C.c_int, _I64, _P]
+        L.orc_qlinear_mult.argtypes = [C.c_float, C.c_float, C.c_float]
+        L.orc_qlinear_mult.restype = C.c_float
+        L.orc_qlinear_requant.argtypes = [_I64, _P, C.c_float, C.c_int32, C.c_int, _P]
         _orc = L
     return _orc
 
@@ -159,6 +162,25 @@ def matmul_integer(a: np.ndarray, b: np.ndarray, za: int, shifted: bool = False)
     fn = lib().orc_matmul_integer_shifted if shifted else lib().orc_matmul_integer
     fn(m, n, k, _p(a), U8 if a.dtype == np.uint8 else I8, za, _p(b), _p(y))
     return y
+
+
+def qlinear_mult(sa: float, sb: float, sy: float) -> float:
+    """QLinearMatMul's multiplier fl32(fl32(sa·sb)/sy) (ops/quant.go:911)."""
+    return float(lib().orc_qlinear_mult(sa, sb, sy))
+
+
+def qlinear_requant(v: np.ndarray, mult: float, zy: int, u8: bool) -> np.ndarray:
+    """QLinearMatMul requantisation of int32 products (ops/quant.go:902-928, satU8/satI8 :26-46)."""
+    v = np.ascontiguousarray(v, np.int32)
+    y = np.empty(v.shape, np.uint8 if u8 else np.int8)
+    lib().orc_qlinear_requant(v.size, _p(v), mult, zy, 1 if u8 else 0, _p(y))
+    return y
+
+
+def qlinear_matmul(a: np.ndarray, b: np.ndarray, za: int, sa: float, sb: float, sy: float, zy: int,
+                   u8: bool) -> np.ndarray:
+    """QLinearMatMul (ops/quant.go:791-928): MatMulInteger, then the requantisation."""
+    return qlinear_requant(matmul_integer(a, b, za), qlinear_mult(sa, sb, sy), zy, u8)
 
 
 def dequantize_linear(x: np.ndarray, scale: np.ndarray, inner: int = 1, zp: np.ndarray = None) -> np.ndarray:

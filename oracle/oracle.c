@@ -175,6 +175,29 @@ void orc_matmul_integer_shifted(int64_t M, int64_t N, int64_t K, const void* A, 
     }
 }
 
+/* satU8 / satI8 (ops/quant.go:26-46) after the requant expression of
+ * qmatmulOp.Run (ops/quant.go:911-925). volatile keeps the product and the
+ * sum separately rounded to f32 whatever the contraction settings. */
+float orc_qlinear_mult(float sa, float sb, float sy) {
+    volatile float ab = sa * sb;
+    volatile float m = ab / sy;
+    return m;
+}
+
+void orc_qlinear_requant(int64_t n, const int32_t* v, float mult, int32_t zy, int u8, void* y) {
+    const float fz = (float)zy;
+    for (int64_t i = 0; i < n; ++i) {
+        volatile float t = (float)v[i] * mult;
+        volatile float u = t + fz;
+        const double r = nearbyint((double)u); /* default rounding mode: half to even */
+        if (u8) {
+            ((uint8_t*)y)[i] = r <= 0 ? 0 : (r >= 255 ? 255 : (uint8_t)r);
+        } else {
+            ((int8_t*)y)[i] = r <= -128 ? -128 : (r >= 127 ? 127 : (int8_t)r);
+        }
+    }
+}
+
 static int32_t int_at(const void* p, int dt, int64_t i) {
     switch (dt) {
         case ORC_U8: return ((const uint8_t*)p)[i];

@@ -70,6 +70,14 @@ void orc_matmul_integer(int64_t M, int64_t N, int64_t K, const void* A, int a_dt
 void orc_matmul_integer_shifted(int64_t M, int64_t N, int64_t K, const void* A, int a_dtype, int32_t za,
                                 const int8_t* B, int32_t* Y);
 
+/* QLinearMatMul requantisation (ops/quant.go:902-928): for each int32
+ * product v (already zero-point corrected),
+ *   y = sat(RoundToEven(fl32(fl32(float32(v)·mult) + zy))),
+ * mult = fl32(fl32(sa·sb)/sy) (orc_qlinear_mult), sat to [0,255] (u8 = 1) or
+ * [-128,127]. The multiply and the add are rounded separately (the
+ * reference's float32 expression as compiled for amd64). Bit-exact. */
+float orc_qlinear_mult(float sa, float sb, float sy);
+void orc_qlinear_requant(int64_t n, const int32_t* v, float mult, int32_t zy, int u8, void* y);
 void orc_dequantize_linear(const void* x, int x_dtype, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
                            const void* zp, int zp_dtype, int64_t n_zp, float* y);
 

@@ -12,6 +12,10 @@ rational arithmetic, independent of oracle/oracle.c:
                    (ops/quant_optest_test.go:194-223: m=7, k=33, n=12,
                    za=110); inputs come from a seeded numpy generator because
                    Go's PCG stream is not reproduced here
+- qlinear_ref      QLinearMatMul's requantisation (ops/quant.go:902-928) of
+                   the matmul_integer product with the scales of the same
+                   reference test; qlinear_ties a power-of-two-scale case that
+                   hits exact .5 ties and both s8 saturation ends
 - bf16_rne         F32ToBF16 (kernels/gemm/bgemm.go:20-26) special cases,
                    expected bits from exact round-half-to-even on rationals
                    plus the NaN rule (quiet bit set, sign kept)
@@ -65,6 +69,19 @@ def bf16_rne_exact(bits: int) -> int:
     return (sign << 15) | r
 
 
+def requant(raw, sa, sb, sy, zy, u8):
+    """satU8/satI8(RoundToEven(fl32(fl32(float32(v)·mult) + zy))), mult = fl32(fl32(sa·sb)/sy): each f32
+    operation rounded by numpy float32 scalars, the integer rounding by Python's round (half to even)."""
+    f = np.float32
+    mult = f(f(f(sa) * f(sb)) / f(sy))
+    lo, hi = (0, 255) if u8 else (-128, 127)
+    out = []
+    for v in raw:
+        u = f(f(f(v) * mult) + f(zy))
+        out.append(min(max(round(float(u)), lo), hi))
+    return out
+
+
 def main():
     kats = {}
     # TestGemmTransB: A=iota(2,3), B=iota(4,3), C=[100..400], alpha=2, beta=1, transB
@@ -89,6 +106,20 @@ def main():
     bv = (rng.integers(0, 256, size=k * n).astype(np.uint8).view(np.int8)).tolist()
     y = [[sum((av[i * k + p] - za) * bv[p * n + j] for p in range(k)) for j in range(n)] for i in range(m)]
     kats["matmul_integer"] = {"m": m, "k": k, "n": n, "za": za, "A": av, "B": bv, "Y": y}
+    # QLinearMatMul requant (ops/quant.go:902-928): the reference test's scales on the same product, and a
+    # power-of-two scale case whose products land on .5 (round half to even) and saturate the s8 range
+    raw = [v for row in y for v in row]
+    kats["qlinear_ref"] = {"raw": raw, "sa": 0.1, "sb": 0.05, "sy": 0.7, "zy": 3, "u8": True,
+                           "Y": requant(raw, 0.1, 0.05, 0.7, 3, True)}
+    rng = np.random.default_rng(2627)
+    m2, k2, n2, za2 = 9, 40, 11, 17
+    a2 = rng.integers(za2 - 3, za2 + 4, size=m2 * k2).tolist()
+    b2 = rng.integers(-3, 4, size=k2 * n2).tolist()
+    raw2 = [sum((a2[i * k2 + p] - za2) * b2[p * n2 + j] for p in range(k2)) for i in range(m2) for j in range(n2)]
+    raw2 += [8, -8, 24, -24, 2040, -2056, 40, 56]  # exact ties and both saturation ends
+    kats["qlinear_ties"] = {"m": m2, "k": k2, "n": n2, "za": za2, "A": a2, "B": b2, "raw": raw2, "sa": 0.25,
+                            "sb": 0.125, "sy": 0.5, "zy": -5, "u8": False,
+                            "Y": requant(raw2, 0.25, 0.125, 0.5, -5, False)}
     # F32ToBF16 special cases
     cases = [0x3F800000, 0x3F808000, 0x3F818000, 0x3F80FFFF, 0x3F807FFF, 0x3F817FFF, 0x00000000, 0x80000000,
              0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001, 0xFF800001, 0x7FBFFFFF, 0x7F7FFFFF, 0xFF7FFFFF,

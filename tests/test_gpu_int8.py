@@ -92,3 +92,43 @@ def test_dequantize_per_axis_exact(sess, xdt, code):
     y = sess.empty(L.DT_F32, x.shape)
     sess.dequantize_linear(sess.to_device(x, code), sess.to_device(sc), y, inner=7, zp=sess.to_device(zp, zcode))
     assert np.array_equal(y.numpy(), oracle.dequantize_linear(x, sc, inner=7, zp=zp))
+
+
+# ---------------- QLinearMatMul (requantised int8 output) ----------------
+
+def test_qlinear_matmul_kats(sess):
+    """The golden requant cases: the reference test's scales (u8 out) and exact .5 ties with s8 saturation."""
+    announce("qlinear kats")
+    km, kr, kt = KATS["matmul_integer"], KATS["qlinear_ref"], KATS["qlinear_ties"]
+    for case, src in [(kr, km), (kt, kt)]:
+        a = np.array(src["A"], np.uint8).reshape(src["m"], src["k"])
+        b = np.array(src["B"], np.int8).reshape(src["k"], src["n"])
+        w = sess.upload_weight(b, trans=False, pack_dtype=L.DT_I8)
+        y = sess.empty(L.DT_U8 if case["u8"] else L.DT_I8, (src["m"], src["n"]))
+        mult = oracle.qlinear_mult(case["sa"], case["sb"], case["sy"])
+        sess.qlinear_matmul(sess.to_device(a), w, src["m"], src["za"], mult, case["zy"], y)
+        want = np.array(case["Y"][:src["m"] * src["n"]], np.int64).reshape(src["m"], src["n"])
+        assert np.array_equal(y.numpy().astype(np.int64), want)
+        w.free()
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 33, 12), (64, 256, 64), (130, 384, 203), (1024, 768, 3072)])
+@pytest.mark.parametrize("a_dt,za,ydt,zy", [(np.uint8, 128, np.uint8, 3), (np.uint8, 77, np.int8, -5),
+                                            (np.int8, -9, np.int8, 0), (np.int8, 0, np.uint8, 128)])
+def test_qlinear_matmul_exact(sess, m, k, n, a_dt, za, ydt, zy):
+    """Bit-exact against the oracle's restatement of the reference requant, ragged and full sizes."""
+    announce(f"qlinear m={m} k={k} n={n} a={np.dtype(a_dt).name} y={np.dtype(ydt).name}")
+    rng = np.random.default_rng(m + 7 * k + 3 * n + zy)
+    lo, hi = (0, 256) if a_dt == np.uint8 else (-128, 128)
+    a = rng.integers(lo, hi, (m, k)).astype(a_dt)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    sa, sb = 0.02, 0.003
+    sy = float(np.float32(sa) * np.float32(sb) * np.float32(np.sqrt(k) * 40.0))  # spreads outputs over the range
+    mult = oracle.qlinear_mult(sa, sb, sy)
+    w = sess.upload_weight(b, trans=False, pack_dtype=L.DT_I8)
+    y = sess.empty(L.DT_U8 if ydt == np.uint8 else L.DT_I8, (m, n))
+    sess.qlinear_matmul(sess.to_device(a), w, m, za, mult, zy, y)
+    want = oracle.qlinear_matmul(a, b, za, sa, sb, sy, zy, ydt == np.uint8)
+    got = y.numpy()
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {got.size} differ"
+    w.free()

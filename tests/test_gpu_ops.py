@@ -181,6 +181,40 @@ def test_gemm_trans_a_and_errors(sess):
         sess.op("Gemm", 11).run(dev(sess, a))
 
 
+def test_qlinear_matmul_op(sess):
+    """TestQLinearMatMulAndMatMulInteger (ops/quant_optest_test.go:194-223), QLinearMatMul half, bit-exact to the
+    oracle's requant; output dtype from y_zero_point; the op's error cases."""
+    announce("op qlinear matmul")
+    km, kr = KATS["matmul_integer"], KATS["qlinear_ref"]
+    a = np.array(km["A"], np.uint8).reshape(km["m"], km["k"])
+    b = np.array(km["B"], np.int8).reshape(km["k"], km["n"])
+    op = sess.op("QLinearMatMul", 10)
+    f32 = lambda v: dev(sess, np.array([v], np.float32))
+    ins = [dev(sess, a), f32(kr["sa"]), dev(sess, np.array([km["za"]], np.uint8)), dev(sess, b), f32(kr["sb"]),
+           dev(sess, np.array([0], np.int8)), f32(kr["sy"]), dev(sess, np.array([kr["zy"]], np.uint8))]
+    (y,) = run(op, *ins)
+    assert y.dtype == np.uint8
+    assert np.array_equal(y.reshape(-1).astype(np.int64), np.array(kr["Y"], np.int64))
+    # s8 output zero point → s8 output
+    ins_s8 = ins[:7] + [dev(sess, np.array([-7], np.int8))]
+    (y8,) = run(op, *ins_s8)
+    assert y8.dtype == np.int8
+    want = oracle.qlinear_matmul(a, b, km["za"], kr["sa"], kr["sb"], kr["sy"], -7, False)
+    assert np.array_equal(y8, want)
+    # absent output zero point → u8, zero point 0
+    (y0,) = run(op, *(ins[:7] + [None]))
+    assert y0.dtype == np.uint8
+    assert np.array_equal(y0, oracle.qlinear_matmul(a, b, km["za"], kr["sa"], kr["sb"], kr["sy"], 0, True))
+    with pytest.raises(IngotError, match="non-zero weight zero_point"):
+        op.run(*(ins[:5] + [dev(sess, np.array([1], np.int8))] + ins[6:]))
+    with pytest.raises(IngotError, match="per-tensor a zero_point only"):
+        op.run(*(ins[:2] + [dev(sess, np.array([1, 2], np.uint8))] + ins[3:]))
+    with pytest.raises(IngotError, match="unsupported output quantization"):
+        op.run(*(ins[:7] + [dev(sess, np.array([1, 2], np.uint8))]))
+    with pytest.raises(IngotError, match="need 8 inputs"):
+        op.run(*ins[:4])
+
+
 def test_matmul_integer_op(sess):
     """TestQLinearMatMulAndMatMulInteger's MatMulInteger half (ops/quant_optest_test.go:194-223)."""
     announce("op matmulinteger")

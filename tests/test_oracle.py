@@ -174,6 +174,38 @@ def test_matmul_integer_s8_and_int64_brute_force():
         assert np.array_equal(oracle.matmul_integer(a, b, za, shifted=True), want)
 
 
+def test_qlinear_requant_kats():
+    """QLinearMatMul requantisation against the golden cases (reference test scales; exact .5 ties, s8 saturation)."""
+    kr = KATS["qlinear_ref"]
+    mult = oracle.qlinear_mult(kr["sa"], kr["sb"], kr["sy"])
+    got = oracle.qlinear_requant(np.array(kr["raw"], np.int32), mult, kr["zy"], kr["u8"])
+    assert np.array_equal(got.astype(np.int64), np.array(kr["Y"], np.int64))
+    # the same product through the whole op, from the matmul_integer inputs
+    km = KATS["matmul_integer"]
+    a = np.array(km["A"], np.uint8).reshape(km["m"], km["k"])
+    b = np.array(km["B"], np.int8).reshape(km["k"], km["n"])
+    full = oracle.qlinear_matmul(a, b, km["za"], kr["sa"], kr["sb"], kr["sy"], kr["zy"], True)
+    assert np.array_equal(full.reshape(-1).astype(np.int64), np.array(kr["Y"], np.int64))
+
+    kt = KATS["qlinear_ties"]
+    a2 = np.array(kt["A"], np.uint8).reshape(kt["m"], kt["k"])
+    b2 = np.array(kt["B"], np.int8).reshape(kt["k"], kt["n"])
+    raw = np.array(kt["raw"], np.int32)
+    mn = kt["m"] * kt["n"]
+    assert np.array_equal(oracle.matmul_integer(a2, b2, kt["za"]).reshape(-1), raw[:mn])
+    mult2 = oracle.qlinear_mult(kt["sa"], kt["sb"], kt["sy"])
+    assert mult2 == 0.0625
+    want = np.array(kt["Y"], np.int64)
+    assert np.array_equal(oracle.qlinear_requant(raw, mult2, kt["zy"], kt["u8"]).astype(np.int64), want)
+
+    # planted mistakes the cases must reject: rounding half away from zero, and truncation toward zero
+    u = raw.astype(np.float32) * np.float32(mult2) + np.float32(kt["zy"])
+    away = np.clip(np.sign(u) * np.floor(np.abs(u) + 0.5), -128, 127).astype(np.int64)
+    assert not np.array_equal(away, want)
+    trunc = np.clip(np.trunc(u), -128, 127).astype(np.int64)
+    assert not np.array_equal(trunc, want)
+
+
 def test_dequantize_kats():
     for name, dt in [("dequantize_u8", np.uint8), ("dequantize_i8", np.int8)]:
         k = KATS[name]
