@@ -270,6 +270,24 @@ class Decode:
             b = 2.0 * n * k + 4.0 * (k + n)
             per[f"{k}x{n}"] = {"us": round(ms * 1e3, 2), "GB_per_s": round(b / (ms * 1e-3) / 1e9, 1)}
         out["m1_per_shape"] = per
+        # the same step on grouped-int8 weights (ingot_weight_quant="int8"): bytes = int8 weights + f32 scales
+        L = self.L
+        wq = [[self.sess.upload_weight(normal32(np.random.default_rng(5 + c), (n, k), 0.02), trans=True,
+                                       pack_dtype=L.PACK_I8G) for k, n in self.shapes] for c in range(self.copies)]
+        i = [0]
+
+        def step_i8g():
+            ws = wq[i[0] % self.copies]
+            i[0] += 1
+            for (k, n), w, y in zip(self.shapes, ws, self.y):
+                self.sess.gemm(self.x[k], w, y, 1)
+        ms = time_steps(self.sess, step_i8g, 60, 10)
+        qbytes = sum(n * k + 4.0 * n * k / 64 + 4.0 * (k + n) for k, n in self.shapes)
+        out["m1_i8g"] = {"GB_per_s": round(qbytes / (ms * 1e-3) / 1e9, 1), "us_per_step": round(ms * 1e3, 2),
+                         "bytes_per_step": qbytes}
+        for cp in wq:
+            for w in cp:
+                w.free()
         return out
 
 

@@ -89,6 +89,11 @@ extern "C" {
 #define INGOT_C_SCALAR 4 /* numel 1 */
 
 /* ---- math type of a GEMM ---- */
+/* Pack type of ingot_rocm_weight_upload beyond the tensor dtypes: int8
+ * weights with one f32 scale per 64 consecutive k of a row, for decode GEMV
+ * (ingot_weight_quant="int8": gemm.I8GWeights, kernels/gemm/i8g.go:12-56). */
+#define INGOT_PACK_I8G 100
+
 #define INGOT_MATH_AUTO 0 /* the weight's packed type: f32 weights → f32 MFMA, bf16 → bf16 MFMA */
 #define INGOT_MATH_F32 1
 #define INGOT_MATH_BF16 2
@@ -146,7 +151,9 @@ int ingot_rocm_timer_stop(ingot_rocm_session* s, float* ms);
  *   src_dtype  : INGOT_DT_F32, INGOT_DT_BF16 (bit patterns) or INGOT_DT_I8.
  *   pack_dtype : INGOT_DT_F32 (from f32), INGOT_DT_BF16 (from f32 by RNE
  *                F32ToBF16, kernels/gemm/bgemm.go:20-26, or from bf16) or
- *                INGOT_DT_I8 (from i8; column sums computed).
+ *                INGOT_DT_I8 (from i8; column sums computed) or
+ *                INGOT_PACK_I8G (from f32 or bf16, K a multiple of 64:
+ *                quantizeI8G, kernels/gemm/i8g.go:33-56).
  *   trans = 1  : the source is [N,K] (Gemm transB=1, nn.Linear); rows = N, cols = K.
  *   trans = 0  : the source is [K,N] (MatMul, Gemm transB=0); rows = K, cols = N.
  *   ld         : source leading dimension in elements (>= cols).

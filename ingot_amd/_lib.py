@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(HERE, "libingot_rocm.so")
 OK, EINVAL, EDECLINED, EDEVICE, ENOMEM = 0, 1, 2, 3, 4
 # dtypes (tensor/dtype.go:12-23)
 DT_F32, DT_F16, DT_BF16, DT_I8, DT_U8, DT_I16, DT_I32, DT_I64, DT_BOOL = 1, 2, 3, 4, 5, 6, 7, 8, 9
+PACK_I8G = 100  # INGOT_PACK_I8G: int8 weights, one f32 scale per 64 k of a row
 # activations
 (ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_GELU_TANH, ACT_SIGMOID, ACT_SILU, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_CLIP,
  ACT_LEAKYRELU) = range(10)

@@ -11,7 +11,8 @@ namespace ingot {
 // lo = bf16(a − hi)) against bf16 weights; two MFMAs per step keep the
 // activation error at ~2⁻¹⁷ relative (f32-class), where KIND_BF16 rounds
 // the activations once (~2⁻⁹).
-enum GemmKind { KIND_BF16 = 0, KIND_F32 = 1, KIND_I8 = 2, KIND_BF16X2 = 3 };
+// KIND_I8G: int8 weights with one f32 scale per 64 k of a row (decode GEMV only).
+enum GemmKind { KIND_BF16 = 0, KIND_F32 = 1, KIND_I8 = 2, KIND_BF16X2 = 3, KIND_I8G = 4 };
 
 // Every kernel row of A and B is read in 128-byte k-tiles: 64 bf16, 32 f32 or
 // 128 int8 elements. Packed operands are zero padded to whole k-tiles.
@@ -73,6 +74,29 @@ hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st);
 // reads: dst holds (split ? 2 : 1) planes of 16·kp elements.
 hipError_t launch_pack_x(const float* x, int64_t ldx, int M, int K, int64_t kp, int split, uint16_t* dst,
                          hipStream_t st);
+
+// Grouped-int8 decode GEMV (gemv_i8g.hip).
+struct I8gArgs {
+    const int8_t* q;   // weight [>= N][ldk], int8
+    const float* sw;   // weight scales [>= N][kp / 64]
+    int64_t ldk, kp;
+    int N, M;          // M <= 4 rows per launch
+    const int8_t* xh;  // activation planes [M][kp] (launch_quantize_x16)
+    const int8_t* xl;
+    const float* sx;   // [M][kp / 64]
+    Epi epi;
+    float* y;
+    int64_t ldy;
+};
+// Quantises a weight (f32 or bf16 bits; trans = 1: [n][k] rows, 0: [k][n])
+// to int8 q[np][ldk] and f32 scales[np][kp / 64] (zero padded).
+hipError_t launch_quantize_i8g(const void* src, int src_dtype, int64_t ld, int trans, int64_t n, int64_t k, int8_t* q,
+                               float* scales, int64_t np, int64_t kp, int64_t ldk, hipStream_t st);
+// Splits x (f32 [M][ldx]) into xh, xl ([M][kp] int8) and sx ([M][kp / 64]).
+hipError_t launch_quantize_x16(const float* x, int64_t ldx, int M, int64_t K, int64_t kp, int8_t* xh, int8_t* xl,
+                               float* sx, hipStream_t st);
+// cfg: weight rows per wave (0: chosen from N).
+hipError_t launch_gemv_i8g(const I8gArgs& a, int cfg, hipStream_t st);
 
 // Packs a weight into [np][kp] of dst_kind, zero padded. src_dtype is an
 // INGOT_DT_* code; trans = 1: src is [n][k] (row pitch ld), 0: src is [k][n].

@@ -336,9 +336,15 @@ class GemmOp : public Op {
     NodeInfo n;
     float alpha, beta;
     bool transA, transB;
-    BCache cache;
+    // quantI8 (ops/matmul.go:19-23): ingot_weight_quant="int8" runs decode
+    // shapes (M <= 4, transB, K % 64 == 0) on an int8 copy of the weight.
+    bool quant_i8 = false;
+    BCache cache, cache_i8;
     ingot_rocm_session* s;
-    ~GemmOp() override { cache.release(s); }
+    ~GemmOp() override {
+        cache.release(s);
+        cache_i8.release(s);
+    }
 
     int run(Ctx& ctx, const std::vector<T>& in) override {
         if (in.size() < 2 || !in[0].present() || !in[1].present()) return n.errorf(INGOT_EINVAL, "need A and B");
@@ -390,10 +396,12 @@ class GemmOp : public Op {
                 ctx.emit(out);
                 return INGOT_OK;
             }
-            const int pack_dt = b.dtype == INGOT_DT_BF16 ? INGOT_DT_BF16 : INGOT_DT_F32;
+            // ops/matmul.go:77-86 (the reference takes it where its int8 dot is SIMD)
+            const bool i8g = quant_i8 && transB && !transA && M <= 4 && K % 64 == 0;
+            const int pack_dt = i8g ? INGOT_PACK_I8G : (b.dtype == INGOT_DT_BF16 ? INGOT_DT_BF16 : INGOT_DT_F32);
             // the weight source is [N,K] when transB (rows = b.dim(0))
             ingot_rocm_weight* w = nullptr;
-            rc = cache.get(s, b, transB ? 1 : 0, pack_dt, &w);
+            rc = (i8g ? cache_i8 : cache).get(s, b, transB ? 1 : 0, pack_dt, &w);
             if (rc) return rc;
             TempWeights tmp(s);
             if (!w) {
@@ -820,6 +828,7 @@ void register_all() {
             op->beta = n.attrs.Float("beta", 1);
             op->transA = n.attrs.Int("transA", 0) != 0;
             op->transB = n.attrs.Int("transB", 0) != 0;
+            op->quant_i8 = n.attrs.String("ingot_weight_quant", "") == "int8";
             op->s = t_build_session;
             *out = std::move(op);
             return INGOT_OK;

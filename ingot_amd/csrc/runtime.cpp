@@ -41,7 +41,7 @@ int elem_size(int dt) {
 
 // elements of a kind per 128-byte k-tile
 int ktile_elems(GemmKind k) { return k == KIND_F32 ? 32 : (k == KIND_I8 ? 128 : 64); }
-int kind_size(GemmKind k) { return k == KIND_F32 ? 4 : (k == KIND_I8 ? 1 : 2); }
+int kind_size(GemmKind k) { return k == KIND_F32 ? 4 : (k == KIND_I8 || k == KIND_I8G ? 1 : 2); }
 
 // Picks the tile configuration with the least estimated time: full rounds of
 // num_cus·occupancy workgroups, each round as long as the most loaded CU.
@@ -208,6 +208,7 @@ int ingot_rocm_close(ingot_rocm_session* s) {
     for (auto* w : s->weights) {
         if (w->data) (void)hipFree(w->data);
         if (w->colsum) (void)hipFree(w->colsum);
+        if (w->gscale) (void)hipFree(w->gscale);
         delete w;
     }
     for (auto& kv : s->buf_class) (void)hipFree(kv.first);
@@ -337,9 +338,13 @@ static int weight_pack(ingot_rocm_session* s, int src_dtype, int pack_dtype, int
     if (pack_dtype == INGOT_DT_F32 && src_dtype == INGOT_DT_F32) kind = KIND_F32;
     else if (pack_dtype == INGOT_DT_BF16 && (src_dtype == INGOT_DT_F32 || src_dtype == INGOT_DT_BF16)) kind = KIND_BF16;
     else if (pack_dtype == INGOT_DT_I8 && src_dtype == INGOT_DT_I8) kind = KIND_I8;
+    else if (pack_dtype == INGOT_PACK_I8G && (src_dtype == INGOT_DT_F32 || src_dtype == INGOT_DT_BF16)) kind = KIND_I8G;
     else return fail(INGOT_EINVAL, "weight: cannot pack dtype %d as %d", src_dtype, pack_dtype);
     const int64_t n = trans ? rows : cols, k = trans ? cols : rows;
     if (n > (int64_t)1 << 30 || k > (int64_t)1 << 30) return fail(INGOT_EINVAL, "weight too large");
+    if (kind == KIND_I8G && k % 64 != 0)
+        return fail(INGOT_EINVAL, "weight: I8G quantisation needs K a multiple of the group size (64), got %lld",
+                    (long long)k);
     auto* w = new ingot_rocm_weight();
     w->pack_dtype = pack_dtype;
     w->kind = kind;
@@ -355,18 +360,24 @@ static int weight_pack(ingot_rocm_session* s, int src_dtype, int pack_dtype, int
     void* tmp = nullptr;
     hipError_t e = hipMalloc(&w->data, (size_t)(w->np * w->ldk) * kind_size(kind));
     if (e == hipSuccess && kind == KIND_I8) e = hipMalloc((void**)&w->colsum, sizeof(int32_t) * w->np);
+    if (e == hipSuccess && kind == KIND_I8G) e = hipMalloc((void**)&w->gscale, sizeof(float) * w->np * (w->kp / 64));
     if (e == hipSuccess && host) {
         e = hipMalloc(&tmp, src_bytes);
         if (e == hipSuccess) e = hipMemcpyAsync(tmp, src, src_bytes, hipMemcpyHostToDevice, s->stream);
         dsrc = tmp;
     }
-    if (e == hipSuccess) e = launch_pack_weight(dsrc, src_dtype, ld, trans, n, k, w->data, kind, w->np, w->kp, w->ldk, s->stream);
+    if (e == hipSuccess && kind == KIND_I8G)
+        e = launch_quantize_i8g(dsrc, src_dtype, ld, trans, n, k, (int8_t*)w->data, w->gscale, w->np, w->kp, w->ldk,
+                                s->stream);
+    else if (e == hipSuccess)
+        e = launch_pack_weight(dsrc, src_dtype, ld, trans, n, k, w->data, kind, w->np, w->kp, w->ldk, s->stream);
     if (e == hipSuccess && kind == KIND_I8) e = launch_colsum_i8((const int8_t*)w->data, w->kp, w->ldk, w->np, w->colsum, s->stream);
     if (host && e == hipSuccess) e = hipStreamSynchronize(s->stream);
     if (tmp) (void)hipFree(tmp);
     if (e != hipSuccess) {
         if (w->data) (void)hipFree(w->data);
         if (w->colsum) (void)hipFree(w->colsum);
+        if (w->gscale) (void)hipFree(w->gscale);
         delete w;
         return hip_fail(e, "weight pack");
     }
@@ -395,6 +406,7 @@ int ingot_rocm_weight_free(ingot_rocm_session* s, ingot_rocm_weight* w) {
     (void)hipStreamSynchronize(s->stream);
     if (w->data) (void)hipFree(w->data);
     if (w->colsum) (void)hipFree(w->colsum);
+    if (w->gscale) (void)hipFree(w->gscale);
     delete w;
     return INGOT_OK;
 }
@@ -443,6 +455,46 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const 
     return INGOT_OK;
 }
 
+// Grouped-int8 GEMV: x split once per call into the workspace, then one
+// launch per 4 activation rows.
+static int run_gemv_i8g(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w) {
+    const int64_t kp = w->kp, gk = kp / 64;
+    if (gk * 4 * 4 * (int64_t)sizeof(float) > 64 * 1024)
+        return fail(INGOT_EDECLINED, "gemm: I8G GEMV supports K up to 65536");
+    void* ws;
+    const size_t plane = (size_t)(a->M * kp);
+    int rc = ws_reserve(s, 2 * plane + (size_t)(a->M * gk) * sizeof(float) + 256, &ws);
+    if (rc) return rc;
+    int8_t* xh = (int8_t*)ws;
+    int8_t* xl = xh + plane;
+    float* sx = (float*)(((uintptr_t)(xl + plane) + 255) & ~(uintptr_t)255);
+    hipError_t e = launch_quantize_x16((const float*)a->d_a, a->lda, (int)a->M, a->K, kp, xh, xl, sx, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize x");
+    for (int64_t m0 = 0; m0 < a->M; m0 += 4) {
+        I8gArgs g;
+        memset(&g, 0, sizeof g);
+        g.q = (const int8_t*)w->data;
+        g.sw = w->gscale;
+        g.ldk = w->ldk;
+        g.kp = kp;
+        g.N = (int)a->N;
+        g.M = (int)std::min<int64_t>(4, a->M - m0);
+        g.xh = xh + m0 * kp;
+        g.xl = xl + m0 * kp;
+        g.sx = sx + m0 * gk;
+        g.epi = make_epi(a);
+        if (g.epi.c_mode == INGOT_C_FULL) g.epi.c += m0 * g.epi.ldc;
+        if (g.epi.c_mode == INGOT_C_COL) g.epi.c += m0;
+        g.y = a->d_y + m0 * a->ldy;
+        g.ldy = a->ldy;
+        int cfg = 0;
+        if (const char* f = getenv("INGOT_I8G_ROWS")) cfg = atoi(f);
+        e = launch_gemv_i8g(g, cfg == 1 || cfg == 2 || cfg == 4 ? cfg : 0, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "i8g gemv launch");
+    }
+    return INGOT_OK;
+}
+
 static int validate_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w) {
     int rc = session_enter(s);
     if (rc) return rc;
@@ -451,6 +503,8 @@ static int validate_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, c
         return fail(INGOT_EINVAL, "gemm: shape M=%lld N=%lld K=%lld does not match weight [%lld,%lld]", (long long)a->M,
                     (long long)a->N, (long long)a->K, (long long)w->n, (long long)w->k);
     if (w->kind == KIND_I8) return fail(INGOT_EINVAL, "gemm: int8 weights run through ingot_rocm_matmul_integer");
+    if (w->kind == KIND_I8G && (a->a_dtype != INGOT_DT_F32 || a->trans_a || a->M > 16 || a->batch > 1))
+        return fail(INGOT_EDECLINED, "gemm: an int8 (I8G) weight serves decode GEMV only: M <= 16 rows of f32 A");
     if (a->a_dtype != INGOT_DT_F32 && a->a_dtype != INGOT_DT_BF16) return fail(INGOT_EINVAL, "gemm: A must be f32 or bf16");
     if (a->M > 0 && (!a->d_a || !a->d_y)) return fail(INGOT_EINVAL, "gemm: nil A or Y");
     const int64_t amin = a->trans_a ? a->M : a->K;
@@ -478,11 +532,14 @@ int ingot_rocm_gemv_bf16(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
 
 // The GEMM after validation. w may be a session weight or a per-call packed
 // operand; stride_b_bytes advances it per batch item (0: shared).
+static int run_gemv_i8g(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w);
+
 static int gemm_core(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w,
                      int64_t stride_b_bytes) {
     int rc;
     const int64_t batch = std::max<int64_t>(1, a->batch);
     if (a->M == 0 || a->N == 0) return INGOT_OK;
+    if (w->kind == KIND_I8G) return run_gemv_i8g(s, a, w);
     if (w->kind == KIND_BF16 && a->M <= 16 && !a->trans_a && a->a_dtype == INGOT_DT_F32 && batch == 1 &&
         !getenv("INGOT_NO_GEMV"))
         return run_gemv(s, a, w);

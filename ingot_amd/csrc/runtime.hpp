@@ -16,6 +16,7 @@ struct ingot_rocm_weight {
     int64_t ldk;             // row pitch in elements (>= kp)
     void* data;
     int32_t* colsum;         // int8 weights: Σ_k W[n][k]
+    float* gscale;           // KIND_I8G: one scale per 64 k of a row, [np][kp / 64]
 };
 
 struct ingot_rocm_session {

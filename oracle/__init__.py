@@ -56,6 +56,11 @@ def lib() -> C.CDLL:
         L.orc_matmul_integer.argtypes = [_I64, _I64, _I64, _P, C.c_int, C.c_int32, _P, _P]
         L.orc_matmul_integer_shifted.argtypes = [_I64, _I64, _I64, _P, C.c_int, C.c_int32, _P, _P]
         L.orc_dequantize_linear.argtypes = [_P, C.c_int, _I64, _P, _I64, _I64, _P, C.c_int, _I64, _P]
+        L.orc_quantize_i8g.argtypes = [_I64, _I64, _P, _I64, _P, _P]
+        L.orc_quantize_x16.argtypes = [_I64, _P, _P, _P, _P]
+        L.orc_dot_q8.argtypes = [_I64, _P, _P, _P, _P, _P]
+        L.orc_dot_q8.restype = C.c_float
+        L.orc_gemv_i8g.argtypes = [_I64, _I64, _I64, _P, _I64, _P, _P, C.c_float, C.c_float, _P, _P]
         L.orc_qlinear_mult.argtypes = [C.c_float, C.c_float, C.c_float]
         L.orc_qlinear_mult.restype = C.c_float
         L.orc_qlinear_requant.argtypes = [_I64, _P, C.c_float, C.c_int32, C.c_int, _P]
@@ -161,6 +166,46 @@ def matmul_integer(a: np.ndarray, b: np.ndarray, za: int, shifted: bool = False)
     y = np.empty((m, n), np.int32)
     fn = lib().orc_matmul_integer_shifted if shifted else lib().orc_matmul_integer
     fn(m, n, k, _p(a), U8 if a.dtype == np.uint8 else I8, za, _p(b), _p(y))
+    return y
+
+
+def quantize_i8g(w: np.ndarray):
+    """quantizeI8G (kernels/gemm/i8g.go:33-56): int8 q [n][k] and f32 scales [n][k/64] of an f32 [n][k] weight."""
+    w = np.ascontiguousarray(w, np.float32)
+    n, k = w.shape
+    q = np.empty((n, k), np.int8)
+    s = np.empty((n, k // 64), np.float32)
+    lib().orc_quantize_i8g(n, k, _p(w), k, _p(q), _p(s))
+    return q, s
+
+
+def quantize_x16(x: np.ndarray):
+    """vek.QuantizeX16 (kernels/vek/scalar.go:38-60): xh, xl (int8) and per-group scales of an f32 vector."""
+    x = np.ascontiguousarray(x, np.float32)
+    k = x.shape[0]
+    xh, xl = np.empty(k, np.int8), np.empty(k, np.int8)
+    sx = np.empty(k // 64, np.float32)
+    lib().orc_quantize_x16(k, _p(x), _p(xh), _p(xl), _p(sx))
+    return xh, xl, sx
+
+
+def dot_q8(w, xh, xl, sx, sw) -> float:
+    """dotQ8Ref (kernels/vek/scalar.go:20-32)."""
+    w, xh, xl = (np.ascontiguousarray(v, np.int8) for v in (w, xh, xl))
+    sx, sw = np.ascontiguousarray(sx, np.float32), np.ascontiguousarray(sw, np.float32)
+    return float(lib().orc_dot_q8(w.size, _p(w), _p(xh), _p(xl), _p(sx), _p(sw)))
+
+
+def gemv_i8g(x: np.ndarray, q: np.ndarray, s: np.ndarray, alpha: float = 1.0, beta: float = 0.0,
+             c: np.ndarray = None) -> np.ndarray:
+    """GemvI8G per row of x (kernels/gemm/i8g.go:70-86); c: C broadcast to [M][N]."""
+    x = np.ascontiguousarray(x, np.float32)
+    q, s = np.ascontiguousarray(q, np.int8), np.ascontiguousarray(s, np.float32)
+    m, k = x.shape
+    n = q.shape[0]
+    cc = None if c is None else np.ascontiguousarray(np.broadcast_to(np.asarray(c, np.float32), (m, n)))
+    y = np.empty((m, n), np.float32)
+    lib().orc_gemv_i8g(m, n, k, _p(x), k, _p(q), _p(s), alpha, beta, _p(cc) if cc is not None else None, _p(y))
     return y
 
 

@@ -14,6 +14,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* F32ToBF16 (kernels/gemm/bgemm.go:20-26): RNE, NaN kept quiet. */
@@ -196,6 +197,84 @@ void orc_qlinear_requant(int64_t n, const int32_t* v, float mult, int32_t zy, in
             ((int8_t*)y)[i] = r <= -128 ? -128 : (r >= 127 ? 127 : (int8_t)r);
         }
     }
+}
+
+void orc_quantize_i8g(int64_t n, int64_t k, const float* w, int64_t ldw, int8_t* q, float* s) {
+    const int64_t gk = k / 64;
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t g = 0; g < gk; ++g) {
+            float amax = 0.f;
+            for (int64_t c = g * 64; c < (g + 1) * 64; ++c) amax = fmaxf(amax, fabsf(w[r * ldw + c]));
+            volatile float sc = amax / 127.f;
+            s[r * gk + g] = sc;
+            for (int64_t c = g * 64; c < (g + 1) * 64; ++c) {
+                int v = 0;
+                if (sc != 0.f) {
+                    volatile float d = w[r * ldw + c] / sc;
+                    const double rr = nearbyint((double)d);
+                    v = rr < -127 ? -127 : (rr > 127 ? 127 : (int)rr);
+                }
+                q[r * k + c] = (int8_t)v;
+            }
+        }
+}
+
+void orc_quantize_x16(int64_t k, const float* x, int8_t* xh, int8_t* xl, float* sx) {
+    const float x16max = 127.f * 128.f;
+    for (int64_t g = 0; g < k / 64; ++g) {
+        float amax = 0.f;
+        for (int64_t i = g * 64; i < (g + 1) * 64; ++i) amax = fmaxf(amax, fabsf(x[i]));
+        volatile float sc = amax / x16max;
+        sx[g] = sc;
+        if (sc == 0.f) {
+            memset(xh + g * 64, 0, 64);
+            memset(xl + g * 64, 0, 64);
+            continue;
+        }
+        volatile float inv = 1.f / sc;
+        for (int64_t i = g * 64; i < (g + 1) * 64; ++i) {
+            volatile float prod = x[i] * inv;
+            double rr = nearbyint((double)prod);
+            int32_t qv = rr < -16256 ? -16256 : (rr > 16256 ? 16256 : (int32_t)rr);
+            const int32_t h = (qv + 64) >> 7;
+            xh[i] = (int8_t)h;
+            xl[i] = (int8_t)(qv - h * 128);
+        }
+    }
+}
+
+float orc_dot_q8(int64_t k, const int8_t* w, const int8_t* xh, const int8_t* xl, const float* sx, const float* sw) {
+    volatile float acc = 0.f;
+    for (int64_t g = 0; g < k / 64; ++g) {
+        int32_t p = 0;
+        for (int64_t i = g * 64; i < (g + 1) * 64; ++i) p += (int32_t)w[i] * (128 * (int32_t)xh[i] + (int32_t)xl[i]);
+        volatile float st = sx[g] * sw[g];
+        volatile float t = st * (float)p;
+        acc = acc + t;
+    }
+    return acc;
+}
+
+void orc_gemv_i8g(int64_t M, int64_t N, int64_t K, const float* x, int64_t ldx, const int8_t* q, const float* s,
+                  float alpha, float beta, const float* c, float* y) {
+    const int64_t gk = K / 64;
+    int8_t* xh = (int8_t*)malloc((size_t)K);
+    int8_t* xl = (int8_t*)malloc((size_t)K);
+    float* sx = (float*)malloc(sizeof(float) * (size_t)(gk ? gk : 1));
+    for (int64_t m = 0; m < M; ++m) {
+        orc_quantize_x16(K, x + m * ldx, xh, xl, sx);
+        for (int64_t j = 0; j < N; ++j) {
+            volatile float v = alpha * orc_dot_q8(K, q + j * K, xh, xl, sx, s + j * gk);
+            if (beta != 0.f && c) {
+                volatile float bc = beta * c[m * N + j];
+                v = v + bc;
+            }
+            y[m * N + j] = v;
+        }
+    }
+    free(xh);
+    free(xl);
+    free(sx);
 }
 
 static int32_t int_at(const void* p, int dt, int64_t i) {

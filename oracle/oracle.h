@@ -78,6 +78,22 @@ void orc_matmul_integer_shifted(int64_t M, int64_t N, int64_t K, const void* A, 
  * reference's float32 expression as compiled for amd64). Bit-exact. */
 float orc_qlinear_mult(float sa, float sb, float sy);
 void orc_qlinear_requant(int64_t n, const int32_t* v, float mult, int32_t zy, int u8, void* y);
+/* Grouped int8 decode GEMV (ingot_weight_quant="int8"), group = 64 k:
+ * orc_quantize_i8g : quantizeI8G (kernels/gemm/i8g.go:33-56) of an [n][k]
+ *   f32 weight: s = max|w|/127 per row-group, q = clamp(RoundToEven(w/s), ±127).
+ * orc_quantize_x16 : vek.QuantizeX16 (kernels/vek/scalar.go:38-60):
+ *   s = max|x|/16256, q = clamp(RoundToEven(x·(1/s)), ±16256),
+ *   xh = (q + 64) >> 7, xl = q − 128·xh.
+ * orc_dot_q8       : dotQ8Ref (kernels/vek/scalar.go:20-32): exact int32
+ *   group sums, acc += (sx·sw)·float32(p) in group order.
+ * orc_gemv_i8g     : GemvI8G (kernels/gemm/i8g.go:70-86) per row of x:
+ *   y = alpha·dot (+ beta·c when beta != 0), c = the broadcast C [M][N].
+ * Each f32 operation is rounded on its own (no contraction). Bit-exact. */
+void orc_quantize_i8g(int64_t n, int64_t k, const float* w, int64_t ldw, int8_t* q, float* s);
+void orc_quantize_x16(int64_t k, const float* x, int8_t* xh, int8_t* xl, float* sx);
+float orc_dot_q8(int64_t k, const int8_t* w, const int8_t* xh, const int8_t* xl, const float* sx, const float* sw);
+void orc_gemv_i8g(int64_t M, int64_t N, int64_t K, const float* x, int64_t ldx, const int8_t* q, const float* s,
+                  float alpha, float beta, const float* c, float* y);
 void orc_dequantize_linear(const void* x, int x_dtype, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
                            const void* zp, int zp_dtype, int64_t n_zp, float* y);
 

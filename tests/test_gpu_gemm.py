@@ -15,6 +15,7 @@ import pytest
 
 import oracle
 from helpers import announce, assert_close, bf16_weights, nstar_tol
+from ingot_amd import IngotError
 from ingot_amd import _lib as L
 
 pytestmark = pytest.mark.gpu
@@ -192,6 +193,65 @@ def test_gemm_dynamic_b_decode_route(sess):
     sess.gemm_dynamic_b(sess.to_device(x), sess.to_device(wb, L.DT_BF16), y, m, n, k, True, k, 0)
     want = oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16)
     assert_close(y.numpy(), want, nstar_tol(k, x, oracle.bf16_to_f32(wb)), "dynamic b gemv")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 9, 16])
+@pytest.mark.parametrize("src", ["f32_nk", "bf16_nk", "f32_kn"])
+@pytest.mark.parametrize("n,k", [(300, 640), (2048, 5632)])
+def test_gemv_i8g_exact(sess, m, src, n, k):
+    """Grouped-int8 decode GEMV (INGOT_PACK_I8G): weight quantisation, activation split, int32 group sums and the
+    in-order f32 chain all equal the oracle's restatement of the reference (GemvI8G) bit for bit."""
+    announce(f"i8g m={m} {src} n={n} k={k}")
+    rng = np.random.default_rng(m * 7 + n + k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    if src.startswith("bf16"):
+        wb = bf16_weights(rng, (n, k), 0.02, "normal")
+        wf = oracle.bf16_to_f32(wb)
+        w = sess.upload_weight(wb, trans=True, pack_dtype=L.PACK_I8G, src_dtype=L.DT_BF16)
+    else:
+        wf = (rng.normal(0, 0.02, (n, k)) * rng.uniform(0.2, 5, (n, 1))).astype(np.float32)
+        w = sess.upload_weight(wf if src == "f32_nk" else np.ascontiguousarray(wf.T), trans=src == "f32_nk",
+                               pack_dtype=L.PACK_I8G)
+    c = rng.normal(0, 1, n).astype(np.float32)
+    y = sess.empty(L.DT_F32, (m, n))
+    sess.gemm(sess.to_device(x), w, y, m, alpha=0.5, beta=2.0, c=sess.to_device(c), c_mode=L.C_ROW)
+    q, sc = oracle.quantize_i8g(wf)
+    want = oracle.gemv_i8g(x, q, sc, 0.5, 2.0, c)
+    got = y.numpy()
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {got.size} differ"
+    w.free()
+
+
+@pytest.mark.parametrize("rows", ["1", "2", "4"])
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_gemv_i8g_rows_per_wave(sess, monkeypatch, rows, m):
+    """Every rows-per-wave variant of the int8 GEMV (INGOT_I8G_ROWS), ragged N, bit-exact."""
+    announce(f"i8g rows={rows} m={m}")
+    monkeypatch.setenv("INGOT_I8G_ROWS", rows)
+    rng = np.random.default_rng(int(rows) * 10 + m)
+    n, k = 301, 1216
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wf = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    w = sess.upload_weight(wf, trans=True, pack_dtype=L.PACK_I8G)
+    y = sess.empty(L.DT_F32, (m, n))
+    sess.gemm(sess.to_device(x), w, y, m)
+    q, sc = oracle.quantize_i8g(wf)
+    assert np.array_equal(y.numpy(), oracle.gemv_i8g(x, q, sc))
+    w.free()
+
+
+def test_gemv_i8g_declines_prefill(sess):
+    """An int8 (I8G) weight serves decode only: M > 16 is declined (the caller keeps its bf16 path)."""
+    announce("i8g declines")
+    rng = np.random.default_rng(3)
+    w = sess.upload_weight(rng.normal(0, 0.02, (64, 128)).astype(np.float32), trans=True, pack_dtype=L.PACK_I8G)
+    y = sess.empty(L.DT_F32, (32, 64))
+    with pytest.raises(IngotError) as e:
+        sess.gemm(sess.to_device(rng.normal(0, 1, (32, 128)).astype(np.float32)), w, y, 32)
+    assert e.value.code == L.EDECLINED
+    with pytest.raises(IngotError, match="multiple of the group size"):
+        sess.upload_weight(rng.normal(0, 0.02, (64, 100)).astype(np.float32), trans=True, pack_dtype=L.PACK_I8G)
+    w.free()
 
 
 @pytest.mark.parametrize("m", [1, 2, 4, 7, 16])

@@ -181,6 +181,34 @@ def test_gemm_trans_a_and_errors(sess):
         sess.op("Gemm", 11).run(dev(sess, a))
 
 
+@pytest.mark.parametrize("m", [1, 3, 9])
+def test_gemm_int8_weight(sess, m):
+    """TestGemmInt8Weight (ops/gemm_bf16_optest_test.go:96-136): ingot_weight_quant="int8" at decode shapes
+    (M <= 4: the int8 GEMV, bit-exact to the oracle and within the reference's bound of the float64 value over
+    the quantised operands); M = 9 stays on the exact bf16 path."""
+    announce(f"op gemm int8 weight m={m}")
+    rng = np.random.default_rng(85 + m)
+    K, N = 256, 29
+    a = rng.uniform(-1, 1, (m, K)).astype(np.float32)
+    wb = bf16_weights(rng, (N, K), 1.0, "uniform")
+    wide = oracle.bf16_to_f32(wb)
+    c = rng.uniform(-1, 1, N).astype(np.float32)
+    op = sess.op("Gemm", 13, {"transB": 1, "alpha": 0.5, "beta": 2.0, "ingot_weight_quant": "int8"})
+    (y,) = run(op, dev(sess, a), dev(sess, wb, L.DT_BF16), dev(sess, c))
+    if m <= 4:
+        q, sc = oracle.quantize_i8g(wide)
+        assert np.array_equal(y, oracle.gemv_i8g(a, q, sc, 0.5, 2.0, c))
+        deq = (q.reshape(N, -1, 64).astype(np.float64) * sc[..., None]).reshape(N, K)
+        for i in range(m):
+            xh, xl, sx = oracle.quantize_x16(a[i])
+            xq = np.repeat(sx, 64).astype(np.float64) * (128 * xh.astype(np.float64) + xl)
+            want = 0.5 * (deq @ xq) + 2.0 * c.astype(np.float64)
+            assert np.all(np.abs(y[i] - want) <= 1e-5 * np.sqrt(K) * (1 + np.abs(want)))
+    else:
+        want = oracle.gemm(a, wb, trans_b=True, b_dtype=oracle.BF16, alpha=0.5, beta=2.0, c=c, c_mode=2)
+        assert_close(y, want, nstar_tol(K, a, wide), "gemm bf16 path")
+
+
 def test_qlinear_matmul_op(sess):
     """TestQLinearMatMulAndMatMulInteger (ops/quant_optest_test.go:194-223), QLinearMatMul half, bit-exact to the
     oracle's requant; output dtype from y_zero_point; the op's error cases."""

@@ -206,6 +206,100 @@ def test_qlinear_requant_kats():
     assert not np.array_equal(trunc, want)
 
 
+def _np_quantize_i8g(w):
+    """quantizeI8G restated independently with vectorised numpy float32 (IEEE division, rint = half-even)."""
+    g = w.reshape(w.shape[0], -1, 64).astype(np.float32)
+    s = (np.abs(g).max(axis=2) / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.where(s[..., None] != 0, np.clip(np.rint(g / s[..., None]), -127, 127), 0)
+    return q.astype(np.int8).reshape(w.shape), s
+
+
+def _np_quantize_x16(x):
+    g = x.reshape(-1, 64).astype(np.float32)
+    s = (np.abs(g).max(axis=1) / np.float32(16256)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        inv = (np.float32(1) / s).astype(np.float32)
+        q = np.where(s[:, None] != 0, np.clip(np.rint((g * inv[:, None]).astype(np.float32)), -16256, 16256), 0)
+    q = q.astype(np.int64)
+    h = (q + 64) >> 7
+    return h.astype(np.int8).reshape(-1), (q - h * 128).astype(np.int8).reshape(-1), s, q.reshape(-1)
+
+
+def test_quantize_i8g_kats_and_numpy():
+    """quantizeI8G: exact-grid groups, .5 ties and a zero group by hand; numpy restatement bit for bit."""
+    g1 = np.arange(-63, 65, 2, dtype=np.float32)[:64]          # odd integers, max |w| = 63
+    g1[0] = -127.0                                               # max 127 → s = 1, q = w
+    g2 = np.array([254.0, 3.0, 5.0, -3.0, -5.0, 7.0] + [2.0] * 58, np.float32)  # s = 2: 1.5→2, 2.5→2, 3.5→4
+    w = np.stack([np.concatenate([g1, g2, np.zeros(64, np.float32)])])
+    q, s = oracle.quantize_i8g(w)
+    assert s.tolist() == [[1.0, 2.0, 0.0]]
+    assert np.array_equal(q[0, :64], g1.astype(np.int8))
+    assert q[0, 64:70].tolist() == [127, 2, 2, -2, -2, 4]
+    assert not q[0, 128:].any()
+    rng = np.random.default_rng(41)
+    w = (rng.normal(0, 0.02, (37, 256)) * rng.uniform(0.1, 10, (37, 1))).astype(np.float32)
+    q, s = oracle.quantize_i8g(w)
+    qn, sn = _np_quantize_i8g(w)
+    assert np.array_equal(q, qn) and np.array_equal(s, sn)
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    err = np.abs(w.reshape(37, 4, 64) - s[..., None] * q.reshape(37, 4, 64).astype(np.float32))
+    assert np.all(err <= 0.5 * s[..., None] * (1 + 1e-5))
+
+
+def test_quantize_x16_invariants_and_numpy():
+    rng = np.random.default_rng(43)
+    x = (rng.normal(0, 1, 512) * np.repeat(rng.uniform(0.01, 100, 8), 64)).astype(np.float32)
+    x[64:128] = 0.0                                              # a zero group
+    xh, xl, sx = oracle.quantize_x16(x)
+    nh, nl, ns, q = _np_quantize_x16(x)
+    assert np.array_equal(xh, nh) and np.array_equal(xl, nl) and np.array_equal(sx, ns)
+    assert np.array_equal(128 * xh.astype(np.int64) + xl, q)
+    assert xl.min() >= -64 and xl.max() <= 63 and np.abs(q).max() <= 16256
+    assert sx[1] == 0 and not xh[64:128].any() and not xl[64:128].any()
+    # planted mistake: the low part taken against 127·h instead of 128·h breaks the split
+    assert not np.array_equal(127 * xh.astype(np.int64) + xl, q)
+
+
+def test_dot_q8_exact_chain():
+    """dotQ8Ref: exact int32 group sums (Python ints), then the f32 chain in group order (numpy float32 scalars)."""
+    rng = np.random.default_rng(47)
+    k = 384
+    w = rng.integers(-127, 128, k).astype(np.int8)
+    x = rng.normal(0, 1, k).astype(np.float32)
+    xh, xl, sx = oracle.quantize_x16(x)
+    sw = rng.uniform(1e-4, 1e-2, k // 64).astype(np.float32)
+    acc = np.float32(0)
+    for g in range(k // 64):
+        p = sum(int(w[i]) * (128 * int(xh[i]) + int(xl[i])) for i in range(g * 64, (g + 1) * 64))
+        acc = np.float32(acc + np.float32(np.float32(sx[g] * sw[g]) * np.float32(p)))
+    assert oracle.dot_q8(w, xh, xl, sx, sw) == float(acc)
+    # planted mistake: the high part without its 128 weight
+    bad = sum(float(sx[g] * sw[g]) * sum(int(w[i]) * (int(xh[i]) + int(xl[i])) for i in range(g * 64, g * 64 + 64))
+              for g in range(k // 64))
+    assert abs(bad - float(acc)) > 1e-3 * abs(float(acc))
+
+
+def test_gemv_i8g_is_close_to_float64():
+    """GemvI8G: the documented approximation (weights' int8 rounding) against the float64 product."""
+    rng = np.random.default_rng(53)
+    m, n, k = 3, 29, 256
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    c = rng.normal(0, 1, n).astype(np.float32)
+    q, s = oracle.quantize_i8g(w)
+    y = oracle.gemv_i8g(x, q, s, 0.5, 2.0, c)
+    deq = (q.reshape(n, 4, 64).astype(np.float64) * s[..., None]).reshape(n, k)
+    rows = []
+    for i in range(m):
+        xh, xl, sx = oracle.quantize_x16(x[i])
+        xq = (np.repeat(sx, 64).astype(np.float64) * (128 * xh.astype(np.float64) + xl))
+        rows.append(0.5 * (deq @ xq) + 2.0 * c)
+    want = np.array(rows)
+    assert np.all(np.abs(y - want) <= 1e-5 * math.sqrt(k) * (1 + np.abs(want)))   # TestGemmInt8Weight's bound
+    assert np.max(np.abs(y - (0.5 * x.astype(np.float64) @ w.T.astype(np.float64) + 2.0 * c))) < 0.02
+
+
 def test_dequantize_kats():
     for name, dt in [("dequantize_u8", np.uint8), ("dequantize_i8", np.int8)]:
         k = KATS[name]
