@@ -204,6 +204,9 @@ typedef struct ingot_rocm_gemm_args {
     int64_t batch;    /* >= 1: strided batch of independent products sharing w */
     int64_t stride_a; /* elements between batch items of A */
     int64_t stride_y; /* elements between batch items of Y */
+    int32_t y_dtype;  /* Y element type: INGOT_DT_F32 (or 0) or INGOT_DT_BF16 (RNE store: a
+                         bf16-resident activation for the next product, GPUBF16
+                         graph/device.go:20-30) */
 } ingot_rocm_gemm_args;
 
 int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* args);
@@ -296,6 +299,37 @@ int ingot_rocm_op_run(ingot_rocm_op* op, int n_in, const ingot_rocm_tensor* in, 
 int ingot_rocm_op_free(ingot_rocm_op* op);
 /* Returns an op output's storage to the session pool (Session.Release). */
 int ingot_rocm_tensor_release(ingot_rocm_session* s, ingot_rocm_tensor* t);
+
+/* ---- Graph session ----
+ * An ONNX node list over the operator layer, compiled with the reference's
+ * GPU-session planning for this path and run on the session stream
+ * (reference: graph.CompileGPU / GPUSession.Run, graph/gpu_other.go:13-37,
+ * graph/gpu_darwin_arm64.go:96-576). Text form, one statement per line:
+ *   input  <name> <dtype> [<d0,d1,...> | ?]
+ *   const  <name> <dtype> <d0,d1,...>      (device data: ingot_rocm_graph_bind)
+ *   node   [<domain>.]<op>[@<opset>] <in,...|_> -> <out,...> [<attrs>]
+ *   output <name>
+ * dtype: f32 bf16 f16 i8 u8 i16 i32 i64 bool; attrs as for ingot_rocm_op_create.
+ * With s = NULL a graph can be created, bound, compiled and described but
+ * not run (planning on a host without a GPU). */
+typedef struct ingot_rocm_graph ingot_rocm_graph;
+#define INGOT_GRAPH_FUSE_BIAS 1 /* fuseMatMulBias (graph/fuse_matmul_bias.go:12-63) */
+#define INGOT_GRAPH_FUSE_ACT 2  /* a product's sole activation consumer in its store (planHalf,
+                                   graph/gpuhalf_darwin_arm64.go:53-73) */
+#define INGOT_GRAPH_HALF 4      /* GPUBF16 (graph/device.go:20-30): bf16 products against constant
+                                   weights, bf16-resident values read only by them */
+int ingot_rocm_graph_create(ingot_rocm_session* s, const char* text, ingot_rocm_graph** out);
+/* Binds a declared constant to device data (same dtype and shape). */
+int ingot_rocm_graph_bind(ingot_rocm_graph* g, const char* name, const ingot_rocm_tensor* t);
+int ingot_rocm_graph_compile(ingot_rocm_graph* g, int flags);
+/* Feeds inputs by name; outputs come back in declaration order as session
+ * pool tensors (release each with ingot_rocm_tensor_release). */
+int ingot_rocm_graph_run(ingot_rocm_graph* g, int n_in, const char* const* names, const ingot_rocm_tensor* in,
+                         int max_out, ingot_rocm_tensor* out, int* n_out);
+/* what = 0: pass statistics ("fuse-act=2;fuse-matmul-bias=2;half-out=1;steps=3;");
+ * what = 1: the compiled steps, one line each. */
+int ingot_rocm_graph_describe(const ingot_rocm_graph* g, int what, char* buf, size_t n);
+int ingot_rocm_graph_free(ingot_rocm_graph* g);
 
 #ifdef __cplusplus
 }

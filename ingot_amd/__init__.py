@@ -8,6 +8,6 @@ build (``build.py``) and a thin Python host wrapper (``host.py``) over the
 C ABI for tests and benchmarks.
 """
 from ._lib import IngotError, load  # noqa: F401
-from .host import DeviceTensor, Op, Session, Weight  # noqa: F401
+from .host import DeviceTensor, Graph, Op, Session, Weight  # noqa: F401
 
-__all__ = ["IngotError", "load", "Session", "Weight", "DeviceTensor", "Op"]
+__all__ = ["IngotError", "load", "Session", "Weight", "DeviceTensor", "Op", "Graph"]

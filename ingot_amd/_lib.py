@@ -17,6 +17,7 @@ OK, EINVAL, EDECLINED, EDEVICE, ENOMEM = 0, 1, 2, 3, 4
 # dtypes (tensor/dtype.go:12-23)
 DT_F32, DT_F16, DT_BF16, DT_I8, DT_U8, DT_I16, DT_I32, DT_I64, DT_BOOL = 1, 2, 3, 4, 5, 6, 7, 8, 9
 PACK_I8G = 100  # INGOT_PACK_I8G: int8 weights, one f32 scale per 64 k of a row
+GRAPH_FUSE_BIAS, GRAPH_FUSE_ACT, GRAPH_HALF = 1, 2, 4  # INGOT_GRAPH_* compile flags
 # activations
 (ACT_NONE, ACT_RELU, ACT_GELU_ERF, ACT_GELU_TANH, ACT_SIGMOID, ACT_SILU, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_CLIP,
  ACT_LEAKYRELU) = range(10)
@@ -36,7 +37,7 @@ class GemmArgs(C.Structure):
         ("act", C.c_int32), ("act_alpha", C.c_float), ("act_beta", C.c_float),
         ("post", C.c_int32), ("post_scale", C.c_float), ("post_shift", C.c_float),
         ("d_y", C.c_void_p), ("ldy", C.c_int64),
-        ("batch", C.c_int64), ("stride_a", C.c_int64), ("stride_y", C.c_int64),
+        ("batch", C.c_int64), ("stride_a", C.c_int64), ("stride_y", C.c_int64), ("y_dtype", C.c_int32),
     ]
 
 
@@ -69,6 +70,13 @@ SIGNATURES = {
     "ingot_rocm_weight_free": (C.c_int, [C.c_void_p, C.c_void_p]),
     "ingot_rocm_weight_info": (C.c_int, [C.c_void_p, C.POINTER(C.c_int64), C.POINTER(C.c_int64),
                                          C.POINTER(C.c_int)]),
+    "ingot_rocm_graph_create": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p)]),
+    "ingot_rocm_graph_bind": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(Tensor)]),
+    "ingot_rocm_graph_compile": (C.c_int, [C.c_void_p, C.c_int]),
+    "ingot_rocm_graph_run": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_char_p), C.POINTER(Tensor), C.c_int,
+                                       C.POINTER(Tensor), C.POINTER(C.c_int)]),
+    "ingot_rocm_graph_describe": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t]),
+    "ingot_rocm_graph_free": (C.c_int, [C.c_void_p]),
     "ingot_rocm_gemm": (C.c_int, [C.c_void_p, C.POINTER(GemmArgs)]),
     "ingot_rocm_gemm_dynamic_b": (C.c_int, [C.c_void_p, C.POINTER(GemmArgs), C.c_void_p, C.c_int32, C.c_int32,
                                             C.c_int64, C.c_int64]),

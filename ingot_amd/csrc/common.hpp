@@ -39,7 +39,16 @@ struct Epi {
     float act_alpha, act_beta;
     int post;
     float post_scale, post_shift;
+    int y_bf16;  // Y stored as bf16 (RNE) instead of f32
 };
+
+// One output element, f32 or bf16 (RNE) per the epilogue.
+__device__ __forceinline__ void store_y(void* y, int64_t i, float v, const Epi& e) {
+    if (e.y_bf16)
+        ((uint16_t*)y)[i] = f32_to_bf16(v);
+    else
+        ((float*)y)[i] = v;
+}
 
 // exp with the argument clamp of expScalar (kernels/vek/scalar.go:7-13).
 __device__ __forceinline__ float exp_clamped(float x) {

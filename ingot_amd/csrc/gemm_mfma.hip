@@ -322,8 +322,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
         ybase = (uintptr_t)(p.qepi.yi ? p.qepi.yi + ybatch : nullptr) | (uintptr_t)(p.qepi.yf ? p.qepi.yf + ybatch : nullptr) |
                 (uintptr_t)(p.qepi.yq ? (uint8_t*)p.qepi.yq + ybatch : nullptr);
     else
-        ybase = (uintptr_t)((float*)p.y + ybatch);
-    const bool vec_ok = (ybase & 15) == 0 && (p.ldy & 3) == 0;
+        ybase = (uintptr_t)p.y + ybatch * (p.epi.y_bf16 ? 2 : 4);
+    // f32: 16-byte stores; bf16: 8-byte stores
+    const bool vec_ok = (ybase & (KD != KIND_I8 && p.epi.y_bf16 ? 7 : 15)) == 0 && (p.ldy & 3) == 0;
 
     if constexpr (KD == KIND_I8) {
         const QEpi& q = p.qepi;
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
         }
         const bool cfull = e.c_mode == INGOT_C_FULL;
         const float ps = e.post ? e.post_scale : 1.f, pt = e.post ? e.post_shift : nz;
-        float* y = (float*)p.y;
+        void* y = p.y;
         auto store_all = [&](auto act) {
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
@@ -438,9 +439,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
                     if (m < p.M && n < p.N) {
                         const int64_t o = ybatch + (int64_t)m * p.ldy + n;
                         if (n + 3 < p.N && vec_ok) {
-                            *(f32x4_t*)(y + o) = v;
+                            if (e.y_bf16) {
+                                const uint32_t lo = f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+                                const uint32_t hi = f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+                                *(uint2*)((uint16_t*)y + o) = make_uint2(lo, hi);
+                            } else {
+                                *(f32x4_t*)((float*)y + o) = v;
+                            }
                         } else {
-                            for (int q = 0; q < 4 && n + q < p.N; ++q) y[o + q] = v[q];
+                            for (int q = 0; q < 4 && n + q < p.N; ++q) store_y(y, o + q, v[q], e);
                         }
                     }
                 }

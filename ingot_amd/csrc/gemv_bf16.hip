@@ -115,7 +115,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemvArgs p) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int n = rb * RB + 4 * g + q;
-        if (n < p.N) p.y[(int64_t)r * p.ldy + n] = epi_apply(p.epi, sum[q], r, n);
+        if (n < p.N) store_y(p.y, (int64_t)r * p.ldy + n, epi_apply(p.epi, sum[q], r, n), p.epi);
     }
 }
 
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows_kernel(GemvArgs p) {
         if (n >= p.N) continue;
 #pragma unroll
         for (int m = 0; m < MM; ++m)
-            if (m < p.M) p.y[(int64_t)m * p.ldy + n] = epi_apply(p.epi, acc[r][m], m, n);
+            if (m < p.M) store_y(p.y, (int64_t)m * p.ldy + n, epi_apply(p.epi, acc[r][m], m, n), p.epi);
     }
 }
 

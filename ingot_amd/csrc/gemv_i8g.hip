@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256) void gemv_i8g_kernel(I8gArgs p) {
     }
     if (e.act != INGOT_ACT_NONE) v = apply_act(v, e.act, e.act_alpha, e.act_beta);
     if (e.post) v = v * e.post_scale + e.post_shift;
-    p.y[(int64_t)m * p.ldy + j] = v;
+    store_y(p.y, (int64_t)m * p.ldy + j, v, e);
 }
 
 template <int R, int MM>

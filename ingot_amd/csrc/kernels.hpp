@@ -65,7 +65,7 @@ struct GemvArgs {
     const uint16_t* xb;
     int64_t xb_plane;
     Epi epi;
-    float* y;
+    void* y;  // f32 or bf16 per epi.y_bf16
     int64_t ldy;
 };
 // cfg selects (waves per workgroup, 16-byte chunks per lane per round).
@@ -85,7 +85,7 @@ struct I8gArgs {
     const int8_t* xl;
     const float* sx;   // [M][kp / 64]
     Epi epi;
-    float* y;
+    void* y;  // f32 or bf16 per epi.y_bf16
     int64_t ldy;
 };
 // Quantises a weight (f32 or bf16 bits; trans = 1: [n][k] rows, 0: [k][n])

@@ -189,6 +189,13 @@ class Op {
    public:
     virtual ~Op() {}
     virtual int run(Ctx& ctx, const std::vector<T>& in) = 0;
+    // A graph plan (graph.cpp): the activation the product's store applies,
+    // bf16 products against constant weights (GPUBF16), a bf16 output.
+    // Only matrix products take one.
+    virtual int plan(int fused_act, bool half, bool out_bf16) {
+        (void)fused_act, (void)half, (void)out_bf16;
+        return INGOT_EDECLINED;
+    }
 };
 
 typedef std::function<int(const NodeInfo&, std::unique_ptr<Op>*)> Builder;
@@ -341,9 +348,15 @@ class GemmOp : public Op {
     bool quant_i8 = false;
     BCache cache, cache_i8;
     ingot_rocm_session* s;
+    int fused_act = INGOT_ACT_NONE;
+    bool half = false, out_bf16 = false;
     ~GemmOp() override {
         cache.release(s);
         cache_i8.release(s);
+    }
+    int plan(int act, bool h, bool ob) override {
+        fused_act = act, half = h, out_bf16 = ob;
+        return INGOT_OK;
     }
 
     int run(Ctx& ctx, const std::vector<T>& in) override {
@@ -351,7 +364,9 @@ class GemmOp : public Op {
         const T& a = in[0];
         const T& b = in[1];
         const bool bf16B = b.dtype == INGOT_DT_BF16 && !transA;
-        if (a.dtype != INGOT_DT_F32 || (b.dtype != INGOT_DT_F32 && !bf16B) || a.rank() != 2 || b.rank() != 2)
+        // a bf16 A is a bf16-resident activation under a half plan
+        const bool a_ok = a.dtype == INGOT_DT_F32 || (half && a.dtype == INGOT_DT_BF16 && !transA);
+        if (!a_ok || (b.dtype != INGOT_DT_F32 && !bf16B) || a.rank() != 2 || b.rank() != 2)
             return n.errorf(INGOT_EINVAL, "need 2-D f32 A and f32 (or bf16 weight) B, got %s %s", a.str().c_str(),
                             b.str().c_str());
         int64_t M = a.dim(0), K = a.dim(1);
@@ -380,13 +395,14 @@ class GemmOp : public Op {
             g.d_c = (const float*)c.data;
             g.beta = beta;
         }
+        const int ydt = out_bf16 ? INGOT_DT_BF16 : INGOT_DT_F32;
         T out;
-        int rc = ctx.new_uninit(INGOT_DT_F32, {M, N}, &out);
+        int rc = ctx.new_uninit(ydt, {M, N}, &out);
         if (rc) return rc;
         if (M > 0 && N > 0) {
             if (K == 0) {
                 // empty reduction: Y = beta·C (or 0)
-                rc = ingot_rocm_memset(s, out.data, 0, (size_t)(M * N * 4));
+                rc = ingot_rocm_memset(s, out.data, 0, (size_t)(M * N * dtype_size(ydt)));
                 if (rc) return rc;
                 if (g.c_mode != INGOT_C_NONE) {
                     ingot_rocm_tensor tmp;
@@ -397,8 +413,9 @@ class GemmOp : public Op {
                 return INGOT_OK;
             }
             // ops/matmul.go:77-86 (the reference takes it where its int8 dot is SIMD)
-            const bool i8g = quant_i8 && transB && !transA && M <= 4 && K % 64 == 0;
-            const int pack_dt = i8g ? INGOT_PACK_I8G : (b.dtype == INGOT_DT_BF16 ? INGOT_DT_BF16 : INGOT_DT_F32);
+            const bool i8g = quant_i8 && transB && !transA && M <= 4 && K % 64 == 0 && a.dtype == INGOT_DT_F32;
+            const int pack_dt =
+                i8g ? INGOT_PACK_I8G : (b.dtype == INGOT_DT_BF16 || half ? INGOT_DT_BF16 : INGOT_DT_F32);
             // the weight source is [N,K] when transB (rows = b.dim(0))
             ingot_rocm_weight* w = nullptr;
             rc = (i8g ? cache_i8 : cache).get(s, b, transB ? 1 : 0, pack_dt, &w);
@@ -412,12 +429,15 @@ class GemmOp : public Op {
             g.N = N;
             g.K = K;
             g.d_a = a.data;
-            g.a_dtype = INGOT_DT_F32;
+            g.a_dtype = a.dtype;
             g.trans_a = transA ? 1 : 0;
             g.lda = a.dim(1);
             g.w = w;
             g.alpha = alpha;
+            g.act = fused_act;
+            if (half && !i8g) g.math = INGOT_MATH_BF16;
             g.d_y = (float*)out.data;
+            g.y_dtype = ydt;
             g.ldy = N;
             rc = ingot_rocm_gemm(s, &g);
             if (rc) return n.errorf(rc, "%s", ingot_rocm_last_error());
@@ -465,7 +485,13 @@ class MatMulOp : public Op {
     BCache cache;
     ingot_rocm_session* s;
     bool bf16_weights = false;
+    int fused_act = INGOT_ACT_NONE;
+    bool half = false, out_bf16 = false;
     ~MatMulOp() override { cache.release(s); }
+    int plan(int act_code, bool h, bool ob) override {
+        fused_act = act_code, half = h, out_bf16 = ob;
+        return INGOT_OK;
+    }
 
     int run(Ctx& ctx, const std::vector<T>& in) override {
         if (in.size() < 2 || in.size() > 3 || !in[0].present() || !in[1].present())
@@ -479,7 +505,9 @@ class MatMulOp : public Op {
                                 shape_str(in[2].shape).c_str());
             bias = (const float*)in[2].data;
         }
-        if (a.dtype != INGOT_DT_F32 || b.dtype != INGOT_DT_F32) return n.errorf(INGOT_EINVAL, "only f32");
+        // a bf16 A is a bf16-resident activation under a half plan
+        if ((a.dtype != INGOT_DT_F32 && !(half && a.dtype == INGOT_DT_BF16)) || b.dtype != INGOT_DT_F32)
+            return n.errorf(INGOT_EINVAL, "only f32");
         Shape as = a.shape, bs = b.shape;
         if (as.empty() || bs.empty()) return n.errorf(INGOT_EINVAL, "scalar operands not allowed");
         bool squeezeM = false, squeezeN = false;
@@ -503,26 +531,31 @@ class MatMulOp : public Op {
         Shape oshape = batch;
         oshape.push_back(M);
         oshape.push_back(N);
+        const int ydt = out_bf16 ? INGOT_DT_BF16 : INGOT_DT_F32;
         T out;
-        rc = ctx.new_uninit(INGOT_DT_F32, oshape, &out);
+        rc = ctx.new_uninit(ydt, oshape, &out);
         if (rc) return rc;
         int64_t nb = numel(batch);
-        const int act_code = act == "gelu" ? INGOT_ACT_GELU_ERF : INGOT_ACT_NONE;
+        const int act_code = act == "gelu" ? INGOT_ACT_GELU_ERF : fused_act;
         if (out.n() > 0) {
             if (K == 0) return n.errorf(INGOT_EDECLINED, "K = 0 is run by the CPU op");
             ingot_rocm_gemm_args g = gemm_args();
             g.K = K;
             g.N = N;
-            g.a_dtype = INGOT_DT_F32;
+            g.a_dtype = a.dtype;
             g.lda = K;
             g.ldy = N;
             g.act = act_code;
+            g.y_dtype = ydt;
+            if (half) g.math = INGOT_MATH_BF16;
             if (bias) {
                 g.d_c = bias;
                 g.c_mode = INGOT_C_ROW;
                 g.beta = 1.f;
             }
-            const int pack_dt = bf16_weights ? INGOT_DT_BF16 : INGOT_DT_F32;
+            const int pack_dt = bf16_weights || half ? INGOT_DT_BF16 : INGOT_DT_F32;
+            if (!batchB.empty() && (a.dtype != INGOT_DT_F32 || ydt != INGOT_DT_F32))
+                return n.errorf(INGOT_EINVAL, "a batched right operand takes f32 operands only");
             if (batchB.empty()) {
                 // 2-D rhs shared by every batch: one GEMM over nb·M rows
                 // (ops/matmul.go:351-361; on the GPU always, the CPU's size
@@ -924,6 +957,13 @@ struct ingot_rocm_op {
     ingot_rocm_session* s;
     std::unique_ptr<ingot::ops::Op> op;
 };
+
+namespace ingot {
+int op_plan(ingot_rocm_op* op, int fused_act, bool half, bool out_bf16) {
+    if (!op) return fail(INGOT_EINVAL, "nil op");
+    return op->op->plan(fused_act, half, out_bf16);
+}
+}  // namespace ingot
 
 using namespace ingot;
 

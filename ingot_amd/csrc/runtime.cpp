@@ -146,11 +146,14 @@ Epi make_epi(const ingot_rocm_gemm_args* a) {
     e.post = a->post;
     e.post_scale = a->post_scale;
     e.post_shift = a->post_shift;
+    e.y_bf16 = a->y_dtype == INGOT_DT_BF16;
     return e;
 }
 
 int check_epi(const ingot_rocm_gemm_args* a) {
     if (a->act < INGOT_ACT_NONE || a->act > INGOT_ACT_LEAKYRELU) return fail(INGOT_EINVAL, "unknown activation %d", a->act);
+    if (a->y_dtype != 0 && a->y_dtype != INGOT_DT_F32 && a->y_dtype != INGOT_DT_BF16)
+        return fail(INGOT_EINVAL, "gemm: Y must be f32 or bf16, got dtype %d", a->y_dtype);
     if (a->d_c && a->beta != 0.f) {
         if (a->c_mode < INGOT_C_NONE || a->c_mode > INGOT_C_SCALAR)
             return fail(INGOT_EINVAL, "unknown C broadcast mode %d", a->c_mode);
@@ -485,7 +488,7 @@ static int run_gemv_i8g(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, co
         g.epi = make_epi(a);
         if (g.epi.c_mode == INGOT_C_FULL) g.epi.c += m0 * g.epi.ldc;
         if (g.epi.c_mode == INGOT_C_COL) g.epi.c += m0;
-        g.y = a->d_y + m0 * a->ldy;
+        g.y = (char*)a->d_y + m0 * a->ldy * (g.epi.y_bf16 ? 2 : 4);
         g.ldy = a->ldy;
         int cfg = 0;
         if (const char* f = getenv("INGOT_I8G_ROWS")) cfg = atoi(f);

@@ -39,6 +39,8 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_fail(hipError_t e, const char* what);
 int session_enter(ingot_rocm_session* s);
 int ws_reserve(ingot_rocm_session* s, size_t bytes, void** out);
+// Applies a graph plan to an op of the operator layer (ops.cpp).
+int op_plan(ingot_rocm_op* op, int fused_act, bool half, bool out_bf16);
 void* pool_get(ingot_rocm_session* s, size_t bytes);
 void pool_put(ingot_rocm_session* s, void* p);
 

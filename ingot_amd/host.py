@@ -199,6 +199,7 @@ class Session:
         g.post_scale, g.post_shift = kw.get("post_scale", 1.0), kw.get("post_shift", 0.0)
         g.d_y, g.ldy = y.ptr, kw.get("ldy", n)
         g.batch, g.stride_a, g.stride_y = kw.get("batch", 1), kw.get("stride_a", 0), kw.get("stride_y", 0)
+        g.y_dtype = y.dtype
         return g
 
     def gemm(self, a: DeviceTensor, w: Weight, y: DeviceTensor, M: int, **kw) -> None:
@@ -246,3 +247,47 @@ class Session:
 
     def op(self, op_type: str, opset: int, attrs: Optional[dict] = None, domain: str = "") -> Op:
         return Op(self, op_type, opset, attrs, domain)
+
+
+class Graph:
+    """A graph session (ingot_rocm_graph_*): an ONNX node list compiled with the reference's GPU-session planning
+    and run through the operator layer. Without a session it can be compiled and described, not run."""
+
+    def __init__(self, sess: Optional[Session], text: str):
+        self.sess = sess
+        self.lib = sess.lib if sess is not None else L.load()
+        h = C.c_void_p()
+        L.check(self.lib.ingot_rocm_graph_create(sess.h if sess is not None else None, text.encode(), C.byref(h)))
+        self.h = h.value
+
+    def bind(self, name: str, t: DeviceTensor) -> None:
+        c = t.as_c()
+        L.check(self.lib.ingot_rocm_graph_bind(self.h, name.encode(), C.byref(c)))
+
+    def compile(self, flags: int = 0) -> None:
+        L.check(self.lib.ingot_rocm_graph_compile(self.h, flags))
+
+    def _describe(self, what: int) -> str:
+        buf = C.create_string_buffer(1 << 16)
+        L.check(self.lib.ingot_rocm_graph_describe(self.h, what, buf, len(buf)))
+        return buf.value.decode()
+
+    def stats(self) -> dict:
+        return {k: int(v) for k, v in (kv.split("=") for kv in self._describe(0).split(";") if kv)}
+
+    def plan(self) -> list:
+        return [ln for ln in self._describe(1).split("\n") if ln]
+
+    def run(self, feeds: dict, max_out: int = 8) -> list:
+        names = (C.c_char_p * max(1, len(feeds)))(*[n.encode() for n in feeds])
+        ins = (L.Tensor * max(1, len(feeds)))(*[t.as_c() for t in feeds.values()])
+        outs = (L.Tensor * max_out)()
+        n = C.c_int()
+        L.check(self.lib.ingot_rocm_graph_run(self.h, len(feeds), names, ins, max_out, outs, C.byref(n)))
+        return [DeviceTensor(self.sess, o.dtype, [o.dims[d] for d in range(o.rank)], o.data, False, True)
+                for o in outs[:n.value]]
+
+    def free(self) -> None:
+        if self.h:
+            L.check(self.lib.ingot_rocm_graph_free(self.h))
+            self.h = None

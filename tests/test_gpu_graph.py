@@ -1,0 +1,103 @@
+"""GPU graph session: the MLP block of the planning tests run end to end on the device.
+
+Reference behaviour mirrored: TestMatMulBias-style fused bias (graph/fuse_matmul_bias.go), planHalf's epilogue
+activations, and GPUBF16's bf16 products with the bound of TestGPUHalfActivations
+(graph/gpuhalf_test.go:85-151: 0.03·max|y| against the f32 result, bit-identical across runs).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from helpers import announce
+from ingot_amd import Graph, IngotError
+from ingot_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+
+MLP = """
+input x f32 {m},{d}
+const W1 f32 {d},{h}
+const b1 f32 {h}
+const W2 f32 {h},{d}
+const b2 f32 {d}
+node MatMul x,W1 -> h1
+node Add h1,b1 -> h2
+node ingot.Gelu h2 -> h3
+node MatMul h3,W2 -> h4
+node Add b2,h4 -> h5
+node Relu h5 -> y
+output y
+"""
+
+
+def mlp_case(sess, m=128, d=768, h=3072, seed=11):
+    rng = np.random.default_rng(seed)
+    ws = {"W1": rng.normal(0, 1 / math.sqrt(d), (d, h)), "b1": rng.normal(0, 0.1, h),
+          "W2": rng.normal(0, 1 / math.sqrt(h), (h, d)), "b2": rng.normal(0, 0.1, d)}
+    ws = {k: v.astype(np.float32) for k, v in ws.items()}
+    x = rng.normal(0, 1, (m, d)).astype(np.float32)
+    dev = {k: sess.to_device(v) for k, v in ws.items()}
+    # float64 chain
+    erf = np.vectorize(math.erf)
+    t = x.astype(np.float64) @ ws["W1"] + ws["b1"]
+    t = 0.5 * t * (1 + erf(t / math.sqrt(2)))
+    y = np.maximum(t @ ws["W2"] + ws["b2"], 0)
+    return MLP.format(m=m, d=d, h=h), dev, sess.to_device(x), y
+
+
+def run_graph(sess, text, dev, x, flags, runs=1):
+    g = Graph(sess, text)
+    for k, v in dev.items():
+        g.bind(k, v)
+    g.compile(flags)
+    outs = []
+    for _ in range(runs):
+        (y,) = g.run({"x": x})
+        assert y.dtype == L.DT_F32
+        outs.append(y.numpy())
+        y.free()
+    st = g.stats()
+    g.free()
+    return outs, st
+
+
+def test_graph_mlp_f32_fusions(sess):
+    announce("graph mlp f32")
+    text, dev, x, want = mlp_case(sess)
+    (y_bias,), st = run_graph(sess, text, dev, x, L.GRAPH_FUSE_BIAS)
+    assert st["fuse-matmul-bias"] == 2 and st["steps"] == 4
+    assert np.max(np.abs(y_bias - want)) <= 1e-4 * max(1.0, np.max(np.abs(want)))
+    # the activations in the products' stores: the same f32 values as the separate activation ops
+    outs, st = run_graph(sess, text, dev, x, L.GRAPH_FUSE_BIAS | L.GRAPH_FUSE_ACT, runs=3)
+    assert st["fuse-act"] == 2 and st["steps"] == 2
+    for y in outs:
+        assert np.array_equal(y, y_bias)
+
+
+def test_graph_mlp_gpubf16(sess):
+    announce("graph mlp gpubf16")
+    text, dev, x, want = mlp_case(sess)
+    outs, st = run_graph(sess, text, dev, x, L.GRAPH_FUSE_BIAS | L.GRAPH_FUSE_ACT | L.GRAPH_HALF, runs=3)
+    assert st["half-out"] == 1
+    d = np.max(np.abs(outs[0] - want))
+    assert d <= 0.03 * np.max(np.abs(want)) and not math.isnan(d)
+    assert d > 1e-4 * np.max(np.abs(want))  # bf16 operands really used
+    assert all(np.array_equal(o, outs[0]) for o in outs[1:])
+
+
+def test_graph_unfused_add_is_declined(sess):
+    announce("graph unsupported op")
+    text, dev, x, _ = mlp_case(sess, m=8, d=64, h=128)
+    g = Graph(sess, text)
+    for k, v in dev.items():
+        g.bind(k, v)
+    with pytest.raises(IngotError, match="Add"):
+        g.compile(0)
+    g.free()
+    with pytest.raises(IngotError, match="not fed"):
+        g2 = Graph(sess, text)
+        for k, v in dev.items():
+            g2.bind(k, v)
+        g2.compile(L.GRAPH_FUSE_BIAS)
+        g2.run({})
