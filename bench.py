@@ -291,6 +291,54 @@ class Decode:
         return out
 
 
+class FfnGraph:
+    """BERT FFN block (configs[1] shapes) as a graph session: MatMul+Add → GELU → MatMul+Add, planned with
+    fuseMatMulBias + epilogue activations in f32, and under GPUBF16 (bf16 products, bf16-resident hidden)."""
+    name = "ffn_graph"
+    TEXT = """
+input x f32 1024,768
+const W1 f32 768,3072
+const b1 f32 3072
+const W2 f32 3072,768
+const b2 f32 768
+node MatMul x,W1 -> h1
+node Add h1,b1 -> h2
+node ingot.Gelu h2 -> h3
+node MatMul h3,W2 -> h4
+node Add h4,b2 -> y
+output y
+"""
+
+    def __init__(self, sess, L):
+        from ingot_amd import Graph
+        self.sess, self.L = sess, L
+        rng = np.random.default_rng(6)
+        self.x = sess.to_device(rng.normal(0, 1, (1024, 768)).astype(np.float32))
+        self.c = {"W1": normal32(rng, (768, 3072), 0.02), "b1": normal32(rng, (3072,), 0.02),
+                  "W2": normal32(rng, (3072, 768), 0.02), "b2": normal32(rng, (768,), 0.02)}
+        self.c = {k: sess.to_device(v) for k, v in self.c.items()}
+        self.graphs = {}
+        base = L.GRAPH_FUSE_BIAS | L.GRAPH_FUSE_ACT
+        for mode, flags in (("f32", base), ("gpubf16", base | L.GRAPH_HALF)):
+            g = Graph(sess, self.TEXT)
+            for k, v in self.c.items():
+                g.bind(k, v)
+            g.compile(flags)
+            self.graphs[mode] = g
+        self.flops = 2 * 2.0 * 1024 * 768 * 3072
+
+    def report(self):
+        out = {}
+        for mode, g in self.graphs.items():
+            def step(g=g):
+                (y,) = g.run({"x": self.x})
+                y.free()
+            ms = time_steps(self.sess, step, 50, 10)
+            out[mode] = {"TFLOPS": round(self.flops / (ms * 1e-3) / 1e12, 2), "us_per_step": round(ms * 1e3, 2),
+                         "plan": g.stats()}
+        return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -353,6 +401,8 @@ def main() -> int:
             extra[cls.name] = w.report(time_steps(sess, w.step, 50, 10))
         log("decode: measuring")
         extra["decode"] = Decode(sess, L).report()
+        log("ffn graph: measuring")
+        extra["ffn_graph"] = FfnGraph(sess, L).report()
         res["workloads"] = extra
     sess.close()
     print(json.dumps(res), flush=True)
