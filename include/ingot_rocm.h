@@ -254,6 +254,40 @@ int ingot_rocm_qlinear_matmul(ingot_rocm_session* s, int64_t M, int64_t N, int64
                               int32_t a_dtype, int64_t lda, int32_t za, const ingot_rocm_weight* w, float mult,
                               int32_t zy, int32_t y_dtype, void* d_y);
 
+/* QLinearConv, 2-D NCHW (qlinearConvOp.Run, ops/quant.go:343-420; requant
+ * qconvRun.corr/requant :441-468):
+ *   v[n,m,oh,ow] = Σ_{cg,kh,kw} W[m,cg,kh,kw]·(x[n, g·Cg+cg, ih, iw] − zx) + bias[m]
+ *     (ih = oh·stride_h + kh·dilation_h − pad_top, iw likewise; taps outside
+ *      the image contribute 0: the reference pads with the zero point)
+ *   Y[n,m,oh,ow] = sat(RoundToEven(fl32(fl32(float32(v)·mult[m]) + zy)))
+ * int32 wrap-around as the reference's accumulators. W is packed as
+ * INGOT_DT_I8 from its [M, C/group·KH·KW] view (rows = M, trans = 1), weight
+ * zero point 0 (s8Weights :285-302). x is u8 or s8 with zero point zx in the
+ * range of its dtype (else INGOT_EDECLINED); d_mult[m] = fl32(fl32(x_scale·
+ * w_scale[m]) / y_scale) (:380-390) is computed by the caller; d_bias may be
+ * NULL. Pads are resolved (auto_pad applied, ops/conv.go:115-136); OH and OW
+ * follow convOut (ops/conv.go:110-113). Y is [N, M, OH, OW] of y_dtype
+ * (INGOT_DT_U8 or INGOT_DT_I8). Large groups run an im2col + int8 MFMA GEMM
+ * (the reference's pointwise / im2colTiled paths, :612-673); depthwise and
+ * narrow groups a direct kernel (:472-598). */
+typedef struct ingot_rocm_qconv_args {
+    int64_t n, c, h, w;   /* x [N, C, H, W] */
+    int64_t m, kh, kw;    /* weight [M, C/group, KH, KW] */
+    int64_t group;
+    int64_t stride_h, stride_w, dilation_h, dilation_w;
+    int64_t pad_top, pad_left, pad_bottom, pad_right;
+    const void* d_x;
+    int32_t x_dtype;
+    int32_t zx;
+    const float* d_mult;    /* [M] */
+    const int32_t* d_bias;  /* [M] or NULL */
+    int32_t zy;
+    int32_t y_dtype;
+    void* d_y;
+} ingot_rocm_qconv_args;
+
+int ingot_rocm_qlinear_conv(ingot_rocm_session* s, const ingot_rocm_qconv_args* args, const ingot_rocm_weight* w);
+
 /* DequantizeLinear over a dense tensor of n elements (ops/quant.go:173-229):
  *   y[i] = float32(x[i] − zp[c]) · scale[c],  c = (i / inner) % n_scale
  * x_dtype U8, I8 or I32; n_scale 1 = per-tensor (then inner is ignored);

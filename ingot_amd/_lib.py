@@ -41,6 +41,18 @@ class GemmArgs(C.Structure):
     ]
 
 
+class QconvArgs(C.Structure):
+    _fields_ = [
+        ("n", C.c_int64), ("c", C.c_int64), ("h", C.c_int64), ("w", C.c_int64),
+        ("m", C.c_int64), ("kh", C.c_int64), ("kw", C.c_int64), ("group", C.c_int64),
+        ("stride_h", C.c_int64), ("stride_w", C.c_int64), ("dilation_h", C.c_int64), ("dilation_w", C.c_int64),
+        ("pad_top", C.c_int64), ("pad_left", C.c_int64), ("pad_bottom", C.c_int64), ("pad_right", C.c_int64),
+        ("d_x", C.c_void_p), ("x_dtype", C.c_int32), ("zx", C.c_int32),
+        ("d_mult", C.c_void_p), ("d_bias", C.c_void_p),
+        ("zy", C.c_int32), ("y_dtype", C.c_int32), ("d_y", C.c_void_p),
+    ]
+
+
 class Tensor(C.Structure):
     _fields_ = [("dtype", C.c_int32), ("rank", C.c_int32), ("dims", C.c_int64 * 8), ("data", C.c_void_p)]
 
@@ -87,6 +99,7 @@ SIGNATURES = {
     "ingot_rocm_matmul_integer": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_int32,
                                             C.c_int64, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                             C.c_int32, C.c_void_p]),
+    "ingot_rocm_qlinear_conv": (C.c_int, [C.c_void_p, C.POINTER(QconvArgs), C.c_void_p]),
     "ingot_rocm_dequantize_linear": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int64, C.c_void_p, C.c_int64,
                                                C.c_int64, C.c_void_p, C.c_int32, C.c_int64, C.c_void_p]),
     "ingot_rocm_activation": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_void_p,

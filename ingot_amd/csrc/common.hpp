@@ -123,6 +123,17 @@ struct QEpi {
     void* yq;
     int yq_u8;  // 1: u8 [0,255]; 0: s8 [-128,127]
     float rq_mult, rq_zy;
+    // QLinearConv (ops/quant.go:441-468): an int32 bias added to the
+    // correction and one multiplier per output column (NULL: none / rq_mult),
+    // both at index col_batch·blockIdx.y + n, like colsum.
+    const int32_t* bias;
+    const float* rq_mults;
+    int32_t col_batch;
+    // conv_p > 0: row m is pixel m % conv_p of image m / conv_p and column n
+    // its channel plane, stored at (m / conv_p)·conv_img + n·conv_p + m % conv_p
+    // (NCHW); yq only.
+    int32_t conv_p;
+    int64_t conv_img;
 };
 
 __device__ __forceinline__ int32_t wrap_mul(int32_t a, int32_t b) {

@@ -328,17 +328,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
 
     if constexpr (KD == KIND_I8) {
         const QEpi& q = p.qepi;
+        const int cb = (int)blockIdx.y * q.col_batch;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const int n = col0 + j * 16;
             if (n >= p.N) continue;
             int32_t corr[4];
-            float sc[4];
+            float sc[4], mu[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int nn = min(n + e, p.N - 1);
-                corr[e] = wrap_mul(q.colsum[nn], q.neg_za);
+                corr[e] = wrap_mul(q.colsum[cb + nn], q.neg_za);
+                if (q.bias) corr[e] = wrap_add(corr[e], q.bias[cb + nn]);
                 sc[e] = q.yf ? q.scale[q.n_scale == 1 ? 0 : nn] : 0.f;
+                mu[e] = q.rq_mults ? q.rq_mults[cb + nn] : q.rq_mult;
             }
             const bool full = n + 3 < p.N;
 #pragma unroll
@@ -370,7 +373,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
                     uint8_t qb[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float t = (float)v[e] * q.rq_mult;
+                        const float t = (float)v[e] * mu[e];
                         const float r = rintf(t + q.rq_zy);
                         const int iv = q.yq_u8 ? (r <= 0.f ? 0 : (r >= 255.f ? 255 : (int)r))
                                                : (r <= -128.f ? -128 : (r >= 127.f ? 127 : (int)r));
@@ -378,7 +381,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
                         packed |= (uint32_t)qb[e] << (8 * e);
                     }
                     uint8_t* yq = (uint8_t*)q.yq;
-                    if (full && vec_ok) {
+                    if (q.conv_p > 0) {
+                        // one byte per channel plane; lanes r = 0..15 fill 16 consecutive pixels
+                        const int img = m / q.conv_p;
+                        const int64_t ob = ybatch + (int64_t)img * q.conv_img + (m - img * q.conv_p);
+                        for (int e = 0; e < 4 && n + e < p.N; ++e) yq[ob + (int64_t)(n + e) * q.conv_p] = qb[e];
+                    } else if (full && vec_ok) {
                         *(uint32_t*)(yq + o) = packed;
                     } else {
                         for (int e = 0; e < 4 && n + e < p.N; ++e) yq[o + e] = qb[e];

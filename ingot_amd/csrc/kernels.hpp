@@ -113,6 +113,20 @@ hipError_t launch_colsum_i8(const int8_t* packed, int64_t kp, int64_t ldk, int64
 hipError_t launch_pack_a(const void* src, int src_dtype, int64_t lda, int trans, int64_t m, int64_t k,
                          int64_t src_stride, void* dst, GemmKind dst_kind, int64_t kl, int64_t dst_stride, int batch,
                          hipStream_t st);
+// QLinearConv geometry (qconv.hip): x [N][C][H][W], weight [M][Cg][KH][KW],
+// G groups (C = G·Cg), resolved top/left pads, output [N][M][OH][OW].
+struct QconvGeom {
+    int N, C, H, W, M, G, Cg, KH, KW, sh, sw, dh, dw, pt, pl, OH, OW;
+};
+// col[grp][row][kgl] bytes for rows = images·OH·OW of x (grid y = G): the raw
+// x bytes of tap k = (c, kh, kw), pad outside the image, 0 for k >= kg.
+// Groups are col_group bytes apart; kgl is a multiple of 16.
+hipError_t launch_qim2col(const void* x, const QconvGeom& g, int rows, int kg, int kgl, uint8_t pad, void* col,
+                          int64_t col_group, hipStream_t st);
+// Direct QLinearConv of every output element (weight rows ldw bytes apart).
+hipError_t launch_qconv_direct(const void* x, int x_u8, const QconvGeom& g, const int8_t* w, int64_t ldw,
+                               const int32_t* bias, const float* mult, int32_t zx, float zy, int y_u8, void* y,
+                               hipStream_t st);
 hipError_t launch_dequant(const void* x, int x_dtype, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
                           const void* zp, int zp_dtype, int64_t n_zp, float* y, hipStream_t st);
 hipError_t launch_activation(const float* x, float* y, int64_t rows, int64_t cols, const float* bias, int act,

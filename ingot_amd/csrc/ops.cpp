@@ -6,7 +6,8 @@
 // so a caller sees the same failures (NodeInfo.Errorf: "Op(name): msg").
 //
 // Ops: Gemm@7 and MatMul@1 (ops/matmul.go:27-139, 305-438, 454-472),
-// MatMulInteger@10 and QLinearMatMul@10 (ops/quant.go:791-928, 942-943), DequantizeLinear@10
+// MatMulInteger@10 and QLinearMatMul@10 (ops/quant.go:791-928, 942-943), QLinearConv@10
+// (ops/quant.go:323-420, 941), DequantizeLinear@10
 // (ops/quant.go:168-230, 947-949), and the activation nodes a GEMM epilogue
 // can absorb: Relu@6, Sigmoid@6, HardSwish@14, LeakyRelu@6, HardSigmoid@6,
 // Gelu@20, ingot.Gelu@1, ingot.SiLU@1 (ops/elementwise.go:486-545).
@@ -29,10 +30,11 @@ namespace ops {
 // ---------------- attributes, NodeInfo ----------------
 
 struct Attr {
-    char kind = 0;  // 'i', 'f', 's'
+    char kind = 0;  // 'i', 'f', 's', 'I' (int list)
     int64_t i = 0;
     float f = 0;
     std::string s;
+    std::vector<int64_t> ints;
 };
 
 struct Attrs {
@@ -53,9 +55,13 @@ struct Attrs {
         auto it = m.find(k);
         return it != m.end() && it->second.kind == 's' ? it->second.s : def;
     }
+    std::vector<int64_t> Ints(const std::string& k, const std::vector<int64_t>& def) const {
+        auto it = m.find(k);
+        return it != m.end() && it->second.kind == 'I' ? it->second.ints : def;
+    }
 };
 
-// Parses "i:transB=1;f:alpha=0.5;s:ingot_act=gelu".
+// Parses "i:transB=1;f:alpha=0.5;s:ingot_act=gelu;I:strides=2,2".
 int parse_attrs(const char* text, Attrs* out) {
     if (!text) return INGOT_OK;
     std::string t(text);
@@ -78,6 +84,21 @@ int parse_attrs(const char* text, Attrs* out) {
             case 'i': a.i = strtoll(val.c_str(), &ep, 10); break;
             case 'f': a.f = strtof(val.c_str(), &ep); break;
             case 's': a.s = val; ep = nullptr; break;
+            case 'I': {
+                ep = nullptr;
+                size_t q = 0;
+                while (q < val.size()) {
+                    size_t c = val.find(',', q);
+                    if (c == std::string::npos) c = val.size();
+                    const std::string v = val.substr(q, c - q);
+                    char* e2 = nullptr;
+                    const long long x = strtoll(v.c_str(), &e2, 10);
+                    if (v.empty() || (e2 && *e2)) return fail(INGOT_EINVAL, "bad attribute value %s", item.c_str());
+                    a.ints.push_back(x);
+                    q = c + 1;
+                }
+                break;
+            }
             default: return fail(INGOT_EINVAL, "bad attribute kind %c", a.kind);
         }
         if (ep && *ep) return fail(INGOT_EINVAL, "bad attribute value %s", item.c_str());
@@ -781,6 +802,193 @@ class MatMulIntegerOp : public Op {
     }
 };
 
+// ---------------- QLinearConv ----------------
+
+// qlinearConvOp (ops/quant.go:323-420) over the conv geometry of buildConv
+// (ops/conv.go:61-108): group, strides, dilations, pads, auto_pad; 1-D
+// attributes lift to 2-D (spatial2D, ops/conv.go:86-99). Inputs x, x_scale,
+// x_zero_point, w, w_scale, w_zero_point, y_scale, y_zero_point[, B].
+class QLinearConvOp : public Op {
+   public:
+    NodeInfo n;
+    ingot_rocm_session* s;
+    int64_t group = 1;
+    int64_t strides[2] = {1, 1}, dilations[2] = {1, 1}, pads[4] = {0, 0, 0, 0};
+    std::string auto_pad;
+    bool three_d = false;
+    std::mutex mu;
+    const void* pack_src = nullptr;
+    int64_t pack_m = -1, pack_k = -1;
+    ingot_rocm_weight* packed = nullptr;
+    ~QLinearConvOp() override {
+        if (packed) ingot_rocm_weight_free(s, packed);
+    }
+
+    int build() {
+        group = n.attrs.Int("group", 1);
+        auto_pad = n.attrs.String("auto_pad", "NOTSET");
+        auto st = n.attrs.Ints("strides", {1, 1});
+        auto di = n.attrs.Ints("dilations", {1, 1});
+        auto pa = n.attrs.Ints("pads", {0, 0, 0, 0});
+        // isConv3D: three spatial dims (ops/conv.go:64-68) build, then Run rejects
+        // the rank-5 input (only 2-D conv)
+        auto ks = n.attrs.Ints("kernel_shape", {});
+        if (ks.size() == 3 || st.size() == 3 || di.size() == 3 || pa.size() == 6) {
+            three_d = true;
+            return INGOT_OK;
+        }
+        if (st.size() == 1) st = {1, st[0]};
+        if (di.size() == 1) di = {1, di[0]};
+        if (pa.size() == 2) pa = {0, pa[0], 0, pa[1]};
+        if (st.size() != 2 || di.size() != 2 || pa.size() != 4) {
+            auto js = [](const std::vector<int64_t>& v) {
+                std::string r = "[";
+                for (size_t i = 0; i < v.size(); ++i) r += (i ? " " : "") + std::to_string(v[i]);
+                return r + "]";
+            };
+            return n.errorf(INGOT_EINVAL, "only 1-D and 2-D conv supported (strides=%s dilations=%s pads=%s)",
+                            js(st).c_str(), js(di).c_str(), js(pa).c_str());
+        }
+        for (int i = 0; i < 2; ++i) strides[i] = st[i], dilations[i] = di[i];
+        for (int i = 0; i < 4; ++i) pads[i] = pa[i];
+        return INGOT_OK;
+    }
+
+    // convOp.resolvePads (ops/conv.go:115-136)
+    int resolve_pads(int64_t h, int64_t w, int64_t kh, int64_t kw, int64_t out[4]) {
+        for (int i = 0; i < 4; ++i) out[i] = pads[i];
+        if (auto_pad == "NOTSET" || auto_pad.empty()) return INGOT_OK;
+        if (auto_pad == "VALID") {
+            for (int i = 0; i < 4; ++i) out[i] = 0;
+            return INGOT_OK;
+        }
+        if (auto_pad != "SAME_UPPER" && auto_pad != "SAME_LOWER")
+            return n.errorf(INGOT_EINVAL, "unsupported auto_pad \"%s\"", auto_pad.c_str());
+        const int64_t in[2] = {h, w}, k[2] = {kh, kw};
+        for (int d = 0; d < 2; ++d) {
+            const int64_t st = strides[d], dl = dilations[d];
+            const int64_t o = (in[d] + st - 1) / st;
+            const int64_t total = std::max<int64_t>(0, (o - 1) * st + dl * (k[d] - 1) + 1 - in[d]);
+            const int64_t a = auto_pad == "SAME_LOWER" ? (total + 1) / 2 : total / 2;
+            out[d] = a;
+            out[d + 2] = total - a;
+        }
+        return INGOT_OK;
+    }
+
+    // the packed [M, K] weight, once per weight storage (qlinearConvOp.fill, ops/quant.go:753-789)
+    int weights(const T& w, int64_t m, int64_t k, ingot_rocm_weight** out) {
+        std::lock_guard<std::mutex> g(mu);
+        if (packed && pack_src == w.data && pack_m == m && pack_k == k) {
+            *out = packed;
+            return INGOT_OK;
+        }
+        if (packed) ingot_rocm_weight_free(s, packed);
+        packed = nullptr;
+        int rc = ingot_rocm_weight_pack_device(s, INGOT_DT_I8, INGOT_DT_I8, m, k, k, 1, w.data, &packed);
+        if (rc) return rc;
+        pack_src = w.data, pack_m = m, pack_k = k;
+        *out = packed;
+        return INGOT_OK;
+    }
+
+    // quantParams (ops/quant.go:50-72): one zero point value and the dtype it names
+    int zero_point(const T* zp, std::vector<int32_t>* z, int* dt) {
+        *dt = INGOT_DT_U8;
+        z->assign(1, 0);
+        if (!zp) return INGOT_OK;
+        *dt = zp->dtype;
+        if (zp->dtype != INGOT_DT_U8 && zp->dtype != INGOT_DT_I8 && zp->dtype != INGOT_DT_I32)
+            return n.errorf(INGOT_EINVAL, "unsupported quantization parameter dtype");
+        return read_ints(s, *zp, z);
+    }
+
+    int run(Ctx& ctx, const std::vector<T>& in) override {
+        if (in.size() < 8) return n.errorf(INGOT_EINVAL, "need 8-9 inputs");
+        auto opt = [&](size_t i) { return in.size() > i && in[i].present() ? &in[i] : nullptr; };
+        for (size_t i : {0, 1, 3, 4, 6})
+            if (!in[i].present()) return n.errorf(INGOT_EINVAL, "need 8-9 inputs");
+        const T &x = in[0], &xScale = in[1], &w = in[3], &wScale = in[4], &yScale = in[6];
+        const T *xZp = opt(2), *wZp = opt(5), *yZp = opt(7), *bias = opt(8);
+        // s8Weights (ops/quant.go:285-302)
+        if (w.dtype != INGOT_DT_I8)
+            return n.errorf(INGOT_EINVAL,
+                            "only s8 weights supported (got %s); u8 weights are not emitted by standard quantizers",
+                            dtype_name(w.dtype));
+        int rc;
+        if (wZp) {
+            if (wZp->dtype != INGOT_DT_I8)
+                return n.errorf(INGOT_EINVAL, "weight zero_point dtype %s unsupported", dtype_name(wZp->dtype));
+            std::vector<int32_t> z;
+            if ((rc = read_ints(s, *wZp, &z))) return rc;
+            for (auto v : z)
+                if (v != 0)
+                    return n.errorf(INGOT_EINVAL, "non-zero weight zero_point unsupported (symmetric s8 weights only)");
+        }
+        std::vector<int32_t> xz, yz;
+        int xdt, ydt;
+        if ((rc = zero_point(xZp, &xz, &xdt)) || (rc = zero_point(yZp, &yz, &ydt))) return rc;
+        if (xz.size() != 1 || yz.size() != 1 || ydt == INGOT_DT_I32)
+            return n.errorf(INGOT_EINVAL, "per-tensor activation/output quantization only");
+        if (three_d || x.rank() != 4 || w.rank() != 4) return n.errorf(INGOT_EINVAL, "only 2-D conv");
+        const int64_t N = x.dim(0), C = x.dim(1), H = x.dim(2), W = x.dim(3);
+        const int64_t M = w.dim(0), Cg = w.dim(1), KH = w.dim(2), KW = w.dim(3);
+        if (group < 1 || C != Cg * group || M % group != 0) return n.errorf(INGOT_EINVAL, "channel mismatch");
+        if (x.dtype != INGOT_DT_U8 && x.dtype != INGOT_DT_I8)
+            return n.errorf(INGOT_EINVAL, "activations must be u8 or s8, got %s", dtype_name(x.dtype));
+        if (ydt != INGOT_DT_U8 && ydt != INGOT_DT_I8)
+            return n.errorf(INGOT_EINVAL, "per-tensor activation/output quantization only");
+        int64_t pd[4];
+        if ((rc = resolve_pads(H, W, KH, KW, pd))) return rc;
+        const int64_t OH = (H + pd[0] + pd[2] - (dilations[0] * (KH - 1) + 1)) / strides[0] + 1;
+        const int64_t OW = (W + pd[1] + pd[3] - (dilations[1] * (KW - 1) + 1)) / strides[1] + 1;
+        if (OH < 0 || OW < 0) return n.errorf(INGOT_EINVAL, "negative output size %lldx%lld", (long long)OH, (long long)OW);
+        if (bias && (bias->dtype != INGOT_DT_I32 || bias->n() != M))
+            return n.errorf(INGOT_EINVAL, "bias must be int32 [%lld], got %s", (long long)M, bias->str().c_str());
+        if (wScale.n() != 1 && wScale.n() != M)
+            return n.errorf(INGOT_EINVAL, "w_scale must have 1 or %lld elements", (long long)M);
+        // requant multipliers x_scale·w_scale[m]/y_scale, each product and
+        // quotient rounded to f32 (ops/quant.go:380-390)
+        float xs, ys;
+        if ((rc = read_f32_first(s, xScale, &xs)) || (rc = read_f32_first(s, yScale, &ys)))
+            return n.errorf(rc, "%s", ingot_rocm_last_error());
+        if (wScale.dtype != INGOT_DT_F32) return n.errorf(INGOT_EINVAL, "w_scale must be f32");
+        std::vector<float> wsc((size_t)wScale.n()), mult((size_t)M);
+        if ((rc = ingot_rocm_memcpy_d2h(s, wsc.data(), wScale.data, wsc.size() * sizeof(float))))
+            return n.errorf(rc, "%s", ingot_rocm_last_error());
+        for (int64_t m = 0; m < M; ++m) {
+            volatile float t = xs * wsc[wsc.size() > 1 ? m : 0];
+            mult[m] = t / ys;
+        }
+        T out;
+        if ((rc = ctx.new_uninit(ydt, {N, M, OH, OW}, &out))) return rc;
+        if (N * M * OH * OW > 0) {
+            ingot_rocm_weight* pw = nullptr;
+            if ((rc = weights(w, M, Cg * KH * KW, &pw))) return n.errorf(rc, "%s", ingot_rocm_last_error());
+            void* dm = pool_get(s, (size_t)M * sizeof(float));
+            if (!dm) return n.errorf(INGOT_ENOMEM, "pool allocation failed");
+            if ((rc = ingot_rocm_memcpy_h2d(s, dm, mult.data(), (size_t)M * sizeof(float)))) {
+                pool_put(s, dm);
+                return n.errorf(rc, "%s", ingot_rocm_last_error());
+            }
+            ingot_rocm_qconv_args a;
+            memset(&a, 0, sizeof a);
+            a.n = N, a.c = C, a.h = H, a.w = W, a.m = M, a.kh = KH, a.kw = KW, a.group = group;
+            a.stride_h = strides[0], a.stride_w = strides[1], a.dilation_h = dilations[0], a.dilation_w = dilations[1];
+            a.pad_top = pd[0], a.pad_left = pd[1], a.pad_bottom = pd[2], a.pad_right = pd[3];
+            a.d_x = x.data, a.x_dtype = x.dtype, a.zx = xz[0];
+            a.d_mult = (const float*)dm;
+            a.d_bias = bias ? (const int32_t*)bias->data : nullptr;
+            a.zy = yz[0], a.y_dtype = ydt, a.d_y = out.data;
+            rc = ingot_rocm_qlinear_conv(s, &a, pw);
+            pool_put(s, dm);  // stream-ordered: a later user queues behind this conv
+            if (rc) return n.errorf(rc, "%s", ingot_rocm_last_error());
+        }
+        ctx.emit(out);
+        return INGOT_OK;
+    }
+};
+
 // ---------------- DequantizeLinear ----------------
 
 // dequantizeLinearOp (ops/quant.go:168-230).
@@ -890,6 +1098,15 @@ void register_all() {
             op->n = n;
             op->requant = true;
             op->s = t_build_session;
+            *out = std::move(op);
+            return INGOT_OK;
+        });
+        Register("", "QLinearConv", 10, [](const NodeInfo& n, std::unique_ptr<Op>* out) {
+            auto op = std::make_unique<QLinearConvOp>();
+            op->n = n;
+            op->s = t_build_session;
+            int rc = op->build();
+            if (rc) return rc;
             *out = std::move(op);
             return INGOT_OK;
         });

@@ -748,6 +748,119 @@ int ingot_rocm_qlinear_matmul(ingot_rocm_session* s, int64_t M, int64_t N, int64
                  y_dtype == INGOT_DT_U8 ? 1 : 0, mult, (float)zy);
 }
 
+// convOut (ops/conv.go:110-113); C++ division truncates toward zero as Go's does.
+static int64_t conv_out(int64_t in, int64_t k, int64_t stride, int64_t dil, int64_t pa, int64_t pb) {
+    return (in + pa + pb - (dil * (k - 1) + 1)) / stride + 1;
+}
+
+int ingot_rocm_qlinear_conv(ingot_rocm_session* s, const ingot_rocm_qconv_args* a, const ingot_rocm_weight* w) {
+    int rc = session_enter(s);
+    if (rc) return rc;
+    if (!a) return fail(INGOT_EINVAL, "qlinear_conv: nil args");
+    if (!w || w->kind != KIND_I8) return fail(INGOT_EINVAL, "qlinear_conv: weight must be packed as int8");
+    if (a->x_dtype != INGOT_DT_U8 && a->x_dtype != INGOT_DT_I8)
+        return fail(INGOT_EINVAL, "qlinear_conv: x must be u8 or s8");
+    if (a->y_dtype != INGOT_DT_U8 && a->y_dtype != INGOT_DT_I8)
+        return fail(INGOT_EINVAL, "qlinear_conv: output must be u8 or s8");
+    if (a->n < 0 || a->c < 1 || a->h < 1 || a->w < 1 || a->m < 1 || a->kh < 1 || a->kw < 1 || a->group < 1)
+        return fail(INGOT_EINVAL, "qlinear_conv: bad dims");
+    if (a->c % a->group != 0 || a->m % a->group != 0) return fail(INGOT_EINVAL, "qlinear_conv: channel mismatch");
+    if (a->stride_h < 1 || a->stride_w < 1 || a->dilation_h < 1 || a->dilation_w < 1 || a->pad_top < 0 ||
+        a->pad_left < 0 || a->pad_bottom < 0 || a->pad_right < 0)
+        return fail(INGOT_EINVAL, "qlinear_conv: strides and dilations must be >= 1, pads >= 0");
+    const int64_t Cg = a->c / a->group, Mg = a->m / a->group, K = Cg * a->kh * a->kw;
+    if (w->n != a->m || w->k != K)
+        return fail(INGOT_EINVAL, "qlinear_conv: weight [%lld,%lld] does not match M=%lld K=%lld", (long long)w->n,
+                    (long long)w->k, (long long)a->m, (long long)K);
+    const int64_t OH = conv_out(a->h, a->kh, a->stride_h, a->dilation_h, a->pad_top, a->pad_bottom);
+    const int64_t OW = conv_out(a->w, a->kw, a->stride_w, a->dilation_w, a->pad_left, a->pad_right);
+    if (OH < 0 || OW < 0) return fail(INGOT_EINVAL, "qlinear_conv: negative output size %lldx%lld", (long long)OH,
+                                      (long long)OW);
+    const bool u8 = a->x_dtype == INGOT_DT_U8;
+    if (u8 ? (a->zx < 0 || a->zx > 255) : (a->zx < -128 || a->zx > 127))
+        return fail(INGOT_EDECLINED, "qlinear_conv: x zero point %d outside the range of x", a->zx);
+    const int64_t P = OH * OW, total = a->n * a->m * P;
+    const int64_t lim = (int64_t)1 << 31;
+    if (a->n * a->c * a->h * a->w >= lim || total >= lim || a->h * a->w >= lim / 8 || a->group > 65535)
+        return fail(INGOT_EDECLINED, "qlinear_conv: tensor larger than 2 GiB");
+    if (total == 0) return INGOT_OK;
+    if (!a->d_x || !a->d_mult || !a->d_y) return fail(INGOT_EINVAL, "qlinear_conv: nil x, mult or y");
+    QconvGeom g;
+    g.N = (int)a->n, g.C = (int)a->c, g.H = (int)a->h, g.W = (int)a->w, g.M = (int)a->m, g.G = (int)a->group;
+    g.Cg = (int)Cg, g.KH = (int)a->kh, g.KW = (int)a->kw, g.sh = (int)a->stride_h, g.sw = (int)a->stride_w;
+    g.dh = (int)a->dilation_h, g.dw = (int)a->dilation_w, g.pt = (int)a->pad_top, g.pl = (int)a->pad_left;
+    g.OH = (int)OH, g.OW = (int)OW;
+    const int yu8 = a->y_dtype == INGOT_DT_U8 ? 1 : 0;
+    // Route: a GEMM needs output-channel and reduction width to fill MFMA
+    // tiles; depthwise and narrow groups run direct. INGOT_QCONV_PATH=1/2
+    // forces direct/GEMM (tests run both routes on the same cases).
+    const char* force = getenv("INGOT_QCONV_PATH");
+    const int path = force && *force ? atoi(force) : 0;
+    const int64_t kgl = round_up(K, 128);
+    const bool gemm = path == 2 || (path != 1 && Mg >= 16 && K >= 32);
+    if (!gemm) {
+        hipError_t e = launch_qconv_direct(a->d_x, u8 ? 1 : 0, g, (const int8_t*)w->data, w->ldk, a->d_bias,
+                                           a->d_mult, a->zx, (float)a->zy, yu8, a->d_y, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "qconv direct");
+        return INGOT_OK;
+    }
+    // Images per chunk: the column matrix of one chunk stays under ~512 MiB
+    // and each group's rows under the 2 GiB buffer-offset limit.
+    const int64_t per_img = P * kgl;
+    if ((P + 256) * kgl >= lim || (w->np + 256) * w->ldk >= lim)
+        return fail(INGOT_EDECLINED, "qlinear_conv: column matrix or weight larger than 2 GiB");
+    int64_t ipc = std::max<int64_t>(1, ((int64_t)512 << 20) / (a->group * per_img));
+    ipc = std::min(ipc, std::max<int64_t>(1, (lim - 256 * kgl) / per_img - 1));
+    ipc = std::min(ipc, a->n);
+    void* ws;
+    rc = ws_reserve(s, (size_t)(a->group * ipc * per_img), &ws);
+    if (rc) return rc;
+    const int cfg0 = pick_config(KIND_I8, ipc * P, Mg, a->group, s->num_cus);
+    const GemmConfig* cf;
+    gemm_configs(KIND_I8, &cf);
+    for (int64_t n0 = 0; n0 < a->n; n0 += ipc) {
+        const int64_t imgs = std::min(ipc, a->n - n0);
+        const int64_t rows = imgs * P;
+        const int64_t col_group = rows * kgl;
+        hipError_t e = launch_qim2col((const uint8_t*)a->d_x + n0 * a->c * a->h * a->w, g, (int)rows, (int)K,
+                                      (int)kgl, (uint8_t)a->zx, ws, col_group, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "qim2col");
+        GemmArgs ga;
+        memset(&ga, 0, sizeof ga);
+        ga.a = (const char*)ws;
+        ga.lda_bytes = kgl;
+        ga.stride_a_bytes = col_group;
+        ga.a_bytes = (uint32_t)col_group;
+        ga.a_xor = u8 ? 1 : 0;
+        ga.b = (const char*)w->data;
+        ga.ldb_bytes = w->ldk;
+        ga.stride_b_bytes = a->group > 1 ? Mg * w->ldk : 0;
+        ga.b_bytes = (uint32_t)(a->group > 1 ? Mg * w->ldk : w->np * w->ldk);
+        ga.b_rows = (int)w->np;
+        ga.M = (int)rows;
+        ga.N = (int)Mg;
+        ga.kt = (int)(kgl / KTILE_BYTES);
+        ga.stride_y = Mg * P;
+        ga.ldy = Mg;
+        ga.qepi.colsum = w->colsum;
+        ga.qepi.neg_za = (int32_t)(0u - (uint32_t)(u8 ? a->zx - 128 : a->zx));
+        ga.qepi.yq = (uint8_t*)a->d_y + n0 * a->m * P;
+        ga.qepi.yq_u8 = yu8;
+        ga.qepi.rq_zy = (float)a->zy;
+        ga.qepi.rq_mults = a->d_mult;
+        ga.qepi.bias = a->d_bias;
+        ga.qepi.col_batch = (int32_t)Mg;
+        ga.qepi.conv_p = (int32_t)P;
+        ga.qepi.conv_img = a->m * P;
+        const int cfg = rows == ipc * P ? cfg0 : pick_config(KIND_I8, rows, Mg, a->group, s->num_cus);
+        ga.tiles_m = (int)((rows + cf[cfg].bm - 1) / cf[cfg].bm);
+        ga.tiles_n = (int)((Mg + cf[cfg].bn - 1) / cf[cfg].bn);
+        e = launch_gemm(KIND_I8, cfg, ga, (int)a->group, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "qconv gemm");
+    }
+    return INGOT_OK;
+}
+
 int ingot_rocm_dequantize_linear(ingot_rocm_session* s, const void* d_x, int32_t x_dtype, int64_t n,
                                  const float* d_scale, int64_t n_scale, int64_t inner, const void* d_zp,
                                  int32_t zp_dtype, int64_t n_zp, float* d_y) {

@@ -111,6 +111,8 @@ def _attr(k: str, v) -> str:
         return f"i:{k}={int(v)}"
     if isinstance(v, (float, np.floating)):
         return f"f:{k}={float(v)!r}"
+    if isinstance(v, (list, tuple)):
+        return f"I:{k}=" + ",".join(str(int(x)) for x in v)
     return f"s:{k}={v}"
 
 
@@ -230,6 +232,25 @@ class Session:
         """QLinearMatMul product requantised to y's dtype (u8 or s8)."""
         L.check(self.lib.ingot_rocm_qlinear_matmul(
             self.h, M, w.n, w.k, a.ptr, a.dtype, lda if lda is not None else w.k, za, w.h, mult, zy, y.dtype, y.ptr))
+
+    def qlinear_conv(self, x: DeviceTensor, zx: int, w: Weight, wshape, mult: DeviceTensor, zy: int,
+                     y: DeviceTensor, bias: Optional[DeviceTensor] = None, group: int = 1, strides=(1, 1),
+                     dilations=(1, 1), pads=(0, 0, 0, 0)) -> None:
+        """QLinearConv (ingot_rocm_qlinear_conv): x [N,C,H,W] u8/s8, w packed from its [M, C/group·KH·KW]
+        view (upload_weight(w.reshape(M, -1), trans=True, pack_dtype=DT_I8)), wshape = (M, C/group, KH, KW),
+        mult [M] f32 on the device, resolved pads (top, left, bottom, right), y [N,M,OH,OW] u8/s8."""
+        a = L.QconvArgs()
+        a.n, a.c, a.h, a.w = x.shape
+        a.m, _, a.kh, a.kw = wshape
+        a.group = group
+        a.stride_h, a.stride_w = strides
+        a.dilation_h, a.dilation_w = dilations
+        a.pad_top, a.pad_left, a.pad_bottom, a.pad_right = pads
+        a.d_x, a.x_dtype, a.zx = x.ptr, x.dtype, zx
+        a.d_mult = mult.ptr
+        a.d_bias = bias.ptr if bias is not None else None
+        a.zy, a.y_dtype, a.d_y = zy, y.dtype, y.ptr
+        L.check(self.lib.ingot_rocm_qlinear_conv(self.h, C.byref(a), w.h))
 
     def dequantize_linear(self, x: DeviceTensor, scale: DeviceTensor, y: DeviceTensor, inner: int = 1,
                           zp: Optional[DeviceTensor] = None) -> None:

@@ -64,6 +64,8 @@ def lib() -> C.CDLL:
         L.orc_qlinear_mult.argtypes = [C.c_float, C.c_float, C.c_float]
         L.orc_qlinear_mult.restype = C.c_float
         L.orc_qlinear_requant.argtypes = [_I64, _P, C.c_float, C.c_int32, C.c_int, _P]
+        L.orc_qlinear_conv.restype = _I64
+        L.orc_qlinear_conv.argtypes = [_P, _P, C.c_int, C.c_int32, _P, _P, _P, C.c_int32, C.c_int, _P]
         _orc = L
     return _orc
 
@@ -226,6 +228,63 @@ def qlinear_matmul(a: np.ndarray, b: np.ndarray, za: int, sa: float, sb: float, 
                    u8: bool) -> np.ndarray:
     """QLinearMatMul (ops/quant.go:791-928): MatMulInteger, then the requantisation."""
     return qlinear_requant(matmul_integer(a, b, za), qlinear_mult(sa, sb, sy), zy, u8)
+
+
+def conv_out(n: int, k: int, stride: int, dil: int, pad_a: int, pad_b: int) -> int:
+    """convOut (ops/conv.go:110-113); Go's division truncates toward zero."""
+    num = n + pad_a + pad_b - (dil * (k - 1) + 1)
+    q = abs(num) // stride
+    return (q if num >= 0 else -q) + 1
+
+
+def resolve_pads(auto_pad: str, pads, strides, dilations, h: int, w: int, kh: int, kw: int):
+    """convOp.resolvePads (ops/conv.go:115-136): (top, left, bottom, right)."""
+    pads = list(pads)
+    if auto_pad in ("NOTSET", ""):
+        return tuple(pads)
+    if auto_pad == "VALID":
+        return (0, 0, 0, 0)
+    if auto_pad not in ("SAME_UPPER", "SAME_LOWER"):
+        raise ValueError(f"unsupported auto_pad {auto_pad!r}")
+    for d, n in enumerate((h, w)):
+        k, s, dl = (kh, kw)[d], strides[d], dilations[d]
+        out = (n + s - 1) // s
+        total = max(0, (out - 1) * s + dl * (k - 1) + 1 - n)
+        a = total // 2 if auto_pad == "SAME_UPPER" else (total + 1) // 2
+        pads[d], pads[d + 2] = a, total - a
+    return tuple(pads)
+
+
+def qconv_mult(xs: float, ws: np.ndarray, ys: float, m: int) -> np.ndarray:
+    """Per-channel requant multipliers fl32(fl32(xs·ws[m])/ys) (ops/quant.go:380-390)."""
+    ws = np.asarray(ws, np.float32).reshape(-1)
+    return np.array([qlinear_mult(xs, float(ws[i if ws.size > 1 else 0]), ys) for i in range(m)], np.float32)
+
+
+def qlinear_conv(x: np.ndarray, zx: int, w: np.ndarray, bias, mult: np.ndarray, zy: int, u8_out: bool, group: int = 1,
+                 strides=(1, 1), dilations=(1, 1), pads=(0, 0, 0, 0)) -> np.ndarray:
+    """QLinearConv (ops/quant.go:343-420, im2col route :642-706, requant :449-468):
+    x [N,C,H,W] u8/s8 with zero point zx, w [M,C/group,KH,KW] s8, bias [M] int32 or None,
+    mult [M] f32 (qconv_mult), resolved pads (top, left, bottom, right) → y [N,M,OH,OW]."""
+    x = np.ascontiguousarray(x)
+    w = np.ascontiguousarray(w, np.int8)
+    mult = np.ascontiguousarray(mult, np.float32)
+    n, c, h, wd = x.shape
+    m, _, kh, kw = w.shape
+    oh = conv_out(h, kh, strides[0], dilations[0], pads[0], pads[2])
+    ow = conv_out(wd, kw, strides[1], dilations[1], pads[1], pads[3])
+    if oh < 0 or ow < 0:
+        raise ValueError("invalid conv geometry")
+    geom = np.array([n, c, h, wd, m, kh, kw, group, strides[0], strides[1], dilations[0], dilations[1], *pads],
+                    np.int64)
+    y = np.empty((n, m, oh, ow), np.uint8 if u8_out else np.int8)
+    b = None if bias is None else np.ascontiguousarray(bias, np.int32)
+    dt = {np.dtype(np.uint8): U8, np.dtype(np.int8): I8}[x.dtype]
+    r = lib().orc_qlinear_conv(_p(geom), _p(x), dt, zx, _p(w), _p(b) if b is not None else None, _p(mult), zy,
+                               1 if u8_out else 0, _p(y))
+    if r < 0:
+        raise ValueError("invalid conv geometry")
+    return y
 
 
 def dequantize_linear(x: np.ndarray, scale: np.ndarray, inner: int = 1, zp: np.ndarray = None) -> np.ndarray:

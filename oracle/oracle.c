@@ -299,3 +299,64 @@ void orc_dequantize_linear(const void* x, int x_dtype, int64_t n, const float* s
         y[i] = (float)d * scale[c];
     }
 }
+
+/* convOut (ops/conv.go:110-113). */
+static int64_t conv_out(int64_t in, int64_t k, int64_t stride, int64_t dil, int64_t pa, int64_t pb) {
+    const int64_t eff = dil * (k - 1) + 1;
+    return (in + pa + pb - eff) / stride + 1;
+}
+
+int64_t orc_qlinear_conv(const int64_t* geom, const void* x, int x_dtype, int32_t zx, const int8_t* w,
+                         const int32_t* bias, const float* mult, int32_t zy, int y_u8, void* y) {
+    const int64_t N = geom[0], C = geom[1], H = geom[2], W = geom[3], M = geom[4], KH = geom[5], KW = geom[6];
+    const int64_t G = geom[7], sh = geom[8], sw = geom[9], dh = geom[10], dw = geom[11];
+    const int64_t pt = geom[12], pl = geom[13], pb = geom[14], pr = geom[15];
+    if (G < 1 || C % G != 0 || M % G != 0 || sh < 1 || sw < 1 || dh < 1 || dw < 1) return -1;
+    const int64_t OH = conv_out(H, KH, sh, dh, pt, pb), OW = conv_out(W, KW, sw, dw, pl, pr);
+    if (OH < 0 || OW < 0) return -1;
+    const int64_t Cg = C / G, Mg = M / G, K = Cg * KH * KW, P = OH * OW;
+    /* shiftToS8: u8 x -> x ^ 0x80 (= x - 128), zx' = zx - 128 */
+    const int u8 = x_dtype == ORC_U8;
+    const int32_t zs = u8 ? zx - 128 : zx;
+    const int8_t pv = (int8_t)zs;
+    int8_t* col = (int8_t*)malloc((size_t)(K > 0 ? K : 1));
+    int32_t* acc = (int32_t*)malloc(sizeof(int32_t) * (size_t)(P > 0 ? P : 1) * (size_t)(Mg > 0 ? Mg : 1));
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t g = 0; g < G; ++g) {
+            for (int64_t i = 0; i < P * Mg; ++i) acc[i] = 0;
+            for (int64_t p = 0; p < P; ++p) {
+                const int64_t oh = p / OW, ow = p % OW;
+                /* qim2colRows: k = (c, kh, kw), c-major within the group */
+                for (int64_t k = 0; k < K; ++k) {
+                    const int64_t c = g * Cg + k / (KH * KW), kh = (k / KW) % KH, kw = k % KW;
+                    const int64_t ih = oh * sh + kh * dh - pt, iw = ow * sw + kw * dw - pl;
+                    int8_t v = pv;
+                    if (ih >= 0 && ih < H && iw >= 0 && iw < W) {
+                        const int64_t xi = ((n * C + c) * H + ih) * W + iw;
+                        v = u8 ? (int8_t)(((const uint8_t*)x)[xi] ^ 0x80) : ((const int8_t*)x)[xi];
+                    }
+                    col[k] = v;
+                }
+                for (int64_t mi = 0; mi < Mg; ++mi) {
+                    uint32_t s = 0;
+                    const int8_t* wr = w + (g * Mg + mi) * K;
+                    for (int64_t k = 0; k < K; ++k) s += (uint32_t)((int32_t)wr[k] * (int32_t)col[k]);
+                    acc[mi * P + p] = (int32_t)s;
+                }
+            }
+            for (int64_t mi = 0; mi < Mg; ++mi) {
+                const int64_t m = g * Mg + mi;
+                uint32_t sumw = 0;
+                for (int64_t k = 0; k < K; ++k) sumw += (uint32_t)(int32_t)w[m * K + k];
+                uint32_t corr = (uint32_t)(-zs) * sumw;
+                if (bias) corr += (uint32_t)bias[m];
+                int32_t* v = acc + mi * P;
+                for (int64_t p = 0; p < P; ++p) v[p] = (int32_t)((uint32_t)v[p] + corr);
+                void* dst = (char*)y + (n * M + m) * P;
+                orc_qlinear_requant(P, v, mult[m], zy, y_u8, dst);
+            }
+        }
+    free(col);
+    free(acc);
+    return P;
+}

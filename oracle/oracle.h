@@ -96,6 +96,19 @@ void orc_gemv_i8g(int64_t M, int64_t N, int64_t K, const float* x, int64_t ldx, 
                   float alpha, float beta, const float* c, float* y);
 void orc_dequantize_linear(const void* x, int x_dtype, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
                            const void* zp, int zp_dtype, int64_t n_zp, float* y);
+/* QLinearConv (ops/quant.go:343-420, qconvRun.corr/requant :441-468, the
+ * im2col path :642-706) along the reference's own route: x shifted to s8
+ * (u8: x ^ 0x80, zx' = zx - 128, shiftToS8 :308-321), taps outside the image
+ * read pv = int8(zx') (:657, :676-690), acc = sum_k w[m][k]·col[k][p] with
+ * int32 wrap-around, corr(m) = -zx'·sumW[m] + bias[m] (:441-447), then
+ *   y = sat(RoundToEven(fl32(fl32(float32(acc + corr)·mult[m]) + zy)))
+ * (vek.RequantU8/I8, kernels/vek/quant_amd64.go:52-70). geom holds
+ * N, C, H, W, M, KH, KW, group, stride_h, stride_w, dil_h, dil_w and the
+ * resolved pads top, left, bottom, right; w is [M][C/group][KH][KW], bias may
+ * be NULL, y is [N][M][OH][OW] with OH/OW from convOut (ops/conv.go:110-113).
+ * Returns OH·OW, or -1 for an invalid geometry. Bit-exact. */
+int64_t orc_qlinear_conv(const int64_t* geom, const void* x, int x_dtype, int32_t zx, const int8_t* w,
+                         const int32_t* bias, const float* mult, int32_t zy, int y_u8, void* y);
 
 #ifdef __cplusplus
 }

@@ -49,19 +49,26 @@ def test_struct_layout_matches_header(tmp_path):
     from ingot_amd import _lib
 
     fields = [f for f, _ in _lib.GemmArgs._fields_]
+    qfields = [f for f, _ in _lib.QconvArgs._fields_]
     src = tmp_path / "layout.c"
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "%s"\nint main(void){\n' % HEADER
-        + 'printf("%zu %zu\\n", sizeof(ingot_rocm_gemm_args), sizeof(ingot_rocm_tensor));\n'
+        + 'printf("%zu %zu %zu\\n", sizeof(ingot_rocm_gemm_args), sizeof(ingot_rocm_tensor), '
+          'sizeof(ingot_rocm_qconv_args));\n'
         + "".join('printf("%%zu\\n", offsetof(ingot_rocm_gemm_args, %s));\n' % f for f in fields)
+        + "".join('printf("%%zu\\n", offsetof(ingot_rocm_qconv_args, %s));\n' % f for f in qfields)
         + "return 0;}\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", str(src), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
     assert int(out[0]) == ctypes.sizeof(_lib.GemmArgs)
     assert int(out[1]) == ctypes.sizeof(_lib.Tensor)
-    for f, off in zip(fields, out[2:]):
+    assert int(out[2]) == ctypes.sizeof(_lib.QconvArgs)
+    offs = out[3:]
+    for f, off in zip(fields, offs[:len(fields)]):
         assert getattr(_lib.GemmArgs, f).offset == int(off), f
+    for f, off in zip(qfields, offs[len(fields):]):
+        assert getattr(_lib.QconvArgs, f).offset == int(off), f
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
