@@ -59,6 +59,14 @@ def build(verbose: bool = False) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
+    # A kernel whose host-side launch stub the compiler silently failed to emit
+    # leaves an undefined symbol that a shared library links anyway.
+    nm = shutil.which("nm")
+    if nm:
+        und = subprocess.run([nm, "-D", "--undefined-only", tmp], capture_output=True, text=True).stdout
+        stubs = [ln for ln in und.splitlines() if "__device_stub__" in ln]
+        if stubs:
+            raise RuntimeError("link left kernel launch stubs undefined:\n" + "\n".join(stubs[:5]))
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")

@@ -295,13 +295,14 @@ def test_gemv_epilogue(sess, m):
     assert_close(y.numpy(), want, nstar_tol(k, x, oracle.bf16_to_f32(wb)), "gemv epilogue")
 
 
-@pytest.mark.parametrize("cfg", ["10", "11", "12", "13", "14", "15", "16", "17", "18", "19",
+@pytest.mark.parametrize("cfg", ["10", "11", "12", "13", "14", "15", "16", "17", "18", "19", "20",
                                  "1", "2", "3", "4", "5", "6", "7"])
 @pytest.mark.parametrize("m", [1, 2, 4, 9, 16])
 def test_gemv_forced_configs(sess, monkeypatch, cfg, m):
     """Every GEMV launch configuration (INGOT_GEMV_CFG) that applies to M, strided x, both math modes."""
     rows_cfg = int(cfg) >= 10
-    mm = {"10": 1, "11": 1, "12": 1, "13": 4, "14": 4, "15": 2, "16": 4, "17": 4, "18": 4, "19": 2}.get(cfg, 16)
+    mm = {"10": 1, "11": 1, "12": 1, "13": 4, "14": 4, "15": 2, "16": 4, "17": 4, "18": 4, "19": 2,
+          "20": 1}.get(cfg, 16)
     if (m > 4) == rows_cfg or m > mm:
         pytest.skip("configuration does not cover this M")
     announce(f"gemv cfg={cfg} m={m}")
