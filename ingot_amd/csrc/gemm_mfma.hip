@@ -23,7 +23,8 @@
 // barrier per k-tile. Tile order is XCD-aware (consecutive tiles of the
 // grouped order run on one XCD's L2) and grouped by GROUP_M tile rows. The
 // epilogue (bias/C, activation, post scale/shift, or the int8 column-sum
-// correction + dequant) runs on the accumulators staged through LDS.
+// correction + dequant) runs on the accumulators in registers; its
+// per-column and per-row terms are staged in LDS during the prologue.
 //
 // Reference counterparts: the packed-B sweep + micro-kernel of
 // kernels/gemm/gemm.go:280-334,431-490 (f32), PackBBF16/widenPanel
@@ -156,8 +157,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
 
     // NS LDS stages (a ring of k-tiles). Rows are 128 bytes, unpadded; the
     // 16-byte chunk c of row r sits at position c ^ swz(r).
-    static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "LDS ring must fit in 160 KiB");
-    __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
+    // Per-column (and, for float outputs, per-row) epilogue terms, staged in
+    // LDS at the start so that their loads overlap the first k-tiles' DMA
+    // instead of following the k-loop. int8: [0] correction −za′·colsum(+bias),
+    // [1] dequant scale, [2] requant multiplier; float: [0] β·C per column
+    // (C_ROW, C_SCALAR) and ep_row β·C per row (C_COL); absent terms are −0.0.
+    // Columns past N repeat column N−1 (their outputs are not stored).
+    constexpr int ECOLS = KD == KIND_I8 ? 3 : 1;
+    constexpr int EROWS = KD == KIND_I8 ? 1 : BM;
+    static_assert(64 * WGM * WGN >= BN && 64 * WGM * WGN >= EROWS, "one thread per staged column and row");
+    constexpr int EXTRA = (ECOLS * BN + EROWS) * 4;
+    // Stages larger than 32 KiB start on 64 KiB boundaries when the ring still
+    // fits (a stage straddling a 64 KiB boundary slowed the k-loop on MI355X).
+    constexpr int SSTRIDE = STAGE > 32768 && NS * 65536 + EXTRA <= 160 * 1024 ? 65536 : STAGE;
+    static_assert(NS >= 2 && NS * SSTRIDE + EXTRA <= 160 * 1024, "LDS must fit in 160 KiB");
+    // One LDS allocation: the ring at offset 0, the staged terms after it.
+    __shared__ __attribute__((aligned(1024))) char lds[NS * SSTRIDE + EXTRA];
+    uint32_t(*ep_col)[BN] = (uint32_t(*)[BN])(lds + NS * SSTRIDE);
+    float* ep_row = (float*)(lds + NS * SSTRIDE + ECOLS * BN * 4);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -278,14 +295,50 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     constexpr int NMF = (KD == KIND_F32 ? 4 : 1) * AP * TM * TN;  // MFMAs per half
     FragA fa0, fa1;
     FragB fb0, fb1;
+    // The epilogue terms: raw loads issued right after k-tile 0's DMA, the
+    // arithmetic and the LDS writes after the rest of the prologue DMA, so the
+    // loads' latency overlaps the DMA (a load's value used in the branch that
+    // loads it would make the compiler wait for it there, before any DMA).
+    uint32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+    dma(lds, 0);
+    if (tid < BN) {
+        const int nn = min(n0 + tid, p.N - 1);
+        if constexpr (KD == KIND_I8) {
+            const QEpi& q = p.qepi;
+            const int cb = (int)blockIdx.y * q.col_batch;
+            r0 = (uint32_t)q.colsum[cb + nn];
+            if (q.bias) r1 = (uint32_t)q.bias[cb + nn];
+            if (q.yf) r2 = __float_as_uint(q.scale[q.n_scale == 1 ? 0 : nn]);
+            r3 = q.rq_mults ? __float_as_uint(q.rq_mults[cb + nn]) : __float_as_uint(q.rq_mult);
+        } else {
+            const Epi& e = p.epi;
+            if (e.c_mode == INGOT_C_ROW || e.c_mode == INGOT_C_SCALAR)
+                r0 = __float_as_uint(e.c[e.c_mode == INGOT_C_ROW ? nn : 0]);
+        }
+    }
+    if (KD != KIND_I8 && tid < EROWS && p.epi.c_mode == INGOT_C_COL)
+        r1 = __float_as_uint(p.epi.c[min(m0 + tid, p.M - 1)]);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) dma(lds + s * STAGE, s);
+    for (int s = 1; s < NS; ++s) dma(lds + s * SSTRIDE, s);
+    if (tid < BN) {
+        if constexpr (KD == KIND_I8) {
+            ep_col[0][tid] = (uint32_t)wrap_add(wrap_mul((int32_t)r0, p.qepi.neg_za), (int32_t)r1);
+            ep_col[1][tid] = r2;
+            ep_col[2][tid] = r3;
+        } else {
+            const int cm = p.epi.c_mode;
+            ep_col[0][tid] = __float_as_uint(cm == INGOT_C_ROW || cm == INGOT_C_SCALAR ? p.epi.beta * __uint_as_float(r0)
+                                                                                      : -0.0f);
+        }
+    }
+    if (KD != KIND_I8 && tid < EROWS)
+        ep_row[tid] = p.epi.c_mode == INGOT_C_COL ? p.epi.beta * __uint_as_float(r1) : -0.0f;
     wait_dma_groups<G, NS>(NS - 1);
-    kloop_barrier();  // k-tile 0 in LDS
+    kloop_barrier();  // k-tile 0 in LDS; epilogue terms staged
     read_frags(lds, 0, fa0, fb0);
     int st = 0;  // ring slot of k-tile kt
     for (int kt = 0; kt < KT; ++kt) {
-        char* cur = lds + st * STAGE;
+        char* cur = lds + st * SSTRIDE;
         const int st1 = st + 1 == NS ? 0 : st + 1;
         read_frags(cur, 1, fa1, fb1);
         mma_all(fa0, fb0);
@@ -295,7 +348,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
         kloop_barrier();  // cur fully read by every wave; k-tile kt+1 landed
         __builtin_amdgcn_sched_barrier(0);
         dma(cur, kt + NS);
-        read_frags(lds + st1 * STAGE, 0, fa0, fb0);  // after the last k-tile: unused
+        read_frags(lds + st1 * SSTRIDE, 0, fa0, fb0);  // after the last k-tile: unused
         mma_all(fa1, fb1);
         interleave<NMF, G, NFR>();
         __builtin_amdgcn_sched_barrier(0);
@@ -328,21 +381,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
 
     if constexpr (KD == KIND_I8) {
         const QEpi& q = p.qepi;
-        const int cb = (int)blockIdx.y * q.col_batch;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const int n = col0 + j * 16;
             if (n >= p.N) continue;
-            int32_t corr[4];
-            float sc[4], mu[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int nn = min(n + e, p.N - 1);
-                corr[e] = wrap_mul(q.colsum[cb + nn], q.neg_za);
-                if (q.bias) corr[e] = wrap_add(corr[e], q.bias[cb + nn]);
-                sc[e] = q.yf ? q.scale[q.n_scale == 1 ? 0 : nn] : 0.f;
-                mu[e] = q.rq_mults ? q.rq_mults[cb + nn] : q.rq_mult;
-            }
+            const int lc = n - n0;  // column within the tile (a multiple of 4)
+            const i32x4_t corr = *(const i32x4_t*)&ep_col[0][lc];
+            const f32x4_t sc = *(const f32x4_t*)&ep_col[1][lc];
+            const f32x4_t mu = *(const f32x4_t*)&ep_col[2][lc];
             const bool full = n + 3 < p.N;
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
@@ -406,22 +452,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
         f32x4_t cn[TN];
         float cm[TM];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) cn[j] = f32x4_t{nz, nz, nz, nz};
+        for (int j = 0; j < TN; ++j) cn[j] = *(const f32x4_t*)&ep_col[0][col0 - n0 + j * 16];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) cm[i] = nz;
-        if (e.c_mode == INGOT_C_ROW) {
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) cn[j][q] = e.beta * e.c[min(col0 + j * 16 + q, p.N - 1)];
-        } else if (e.c_mode == INGOT_C_SCALAR) {
-            const float c0 = e.beta * e.c[0];
-#pragma unroll
-            for (int j = 0; j < TN; ++j) cn[j] = f32x4_t{c0, c0, c0, c0};
-        } else if (e.c_mode == INGOT_C_COL) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i) cm[i] = e.beta * e.c[min(row0 + i * 16, p.M - 1)];
-        }
+        for (int i = 0; i < TM; ++i) cm[i] = ep_row[row0 - m0 + i * 16];
         const bool cfull = e.c_mode == INGOT_C_FULL;
         const float ps = e.post ? e.post_scale : 1.f, pt = e.post ? e.post_shift : nz;
         void* y = p.y;
@@ -488,7 +521,8 @@ const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128
                                 {64, 64, 4, 0.60f}, {192, 256, 1, 0.95f}};
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}};
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}};
-const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f}};
+const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f},
+                              {64, 64, 3, 0.5f}, {64, 64, 2, 0.5f}};
 
 template <int KD, int BM, int BN, int WGM, int WGN, int NS>
 hipError_t launch_one(const GemmArgs& a, int batch, hipStream_t st) {
@@ -541,6 +575,8 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 1: return launch_one<KIND_I8, 128, 128, 2, 2, 2>(a, batch, st);
                 case 2: return launch_one<KIND_I8, 128, 64, 2, 2, 2>(a, batch, st);
                 case 3: return launch_one<KIND_I8, 64, 64, 2, 2, 2>(a, batch, st);
+                case 4: return launch_one<KIND_I8, 64, 64, 2, 2, 3>(a, batch, st);
+                case 5: return launch_one<KIND_I8, 64, 64, 2, 2, 4>(a, batch, st);
             }
             break;
     }
