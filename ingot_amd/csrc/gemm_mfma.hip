@@ -519,10 +519,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
 // workgroups) hides latency better than a deeper ring (measured on MI355X).
 const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128, 128, 2, 0.80f}, {128, 64, 3, 0.78f},
                                 {64, 64, 4, 0.60f}, {192, 256, 1, 0.95f}};
-const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}};
+// f32 32×96: on MI355X 15% faster than 64×64 over the BERT projections (M = 1024;
+// N = 768 gives exactly 256 tiles), slightly slower on ties, so weighted 0.97.
+const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}, {32, 96, 4, 0.97f}};
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}};
-const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f},
-                              {64, 64, 3, 0.5f}, {64, 64, 2, 0.5f}};
+const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f}};
 
 template <int KD, int BM, int BN, int WGM, int WGN, int NS>
 hipError_t launch_one(const GemmArgs& a, int batch, hipStream_t st) {
@@ -567,6 +568,7 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 0: return launch_one<KIND_F32, 128, 128, 2, 2, 2>(a, batch, st);
                 case 1: return launch_one<KIND_F32, 128, 64, 2, 2, 2>(a, batch, st);
                 case 2: return launch_one<KIND_F32, 64, 64, 2, 2, 2>(a, batch, st);
+                case 3: return launch_one<KIND_F32, 32, 96, 2, 2, 2>(a, batch, st);
             }
             break;
         case KIND_I8:
@@ -575,8 +577,6 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 1: return launch_one<KIND_I8, 128, 128, 2, 2, 2>(a, batch, st);
                 case 2: return launch_one<KIND_I8, 128, 64, 2, 2, 2>(a, batch, st);
                 case 3: return launch_one<KIND_I8, 64, 64, 2, 2, 2>(a, batch, st);
-                case 4: return launch_one<KIND_I8, 64, 64, 2, 2, 3>(a, batch, st);
-                case 5: return launch_one<KIND_I8, 64, 64, 2, 2, 4>(a, batch, st);
             }
             break;
     }

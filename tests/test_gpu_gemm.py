@@ -295,6 +295,51 @@ def test_gemv_epilogue(sess, m):
     assert_close(y.numpy(), want, nstar_tol(k, x, oracle.bf16_to_f32(wb)), "gemv epilogue")
 
 
+# Every tile configuration of every GEMM kind (INGOT_GEMM_CFG), on shapes with
+# ragged edges in M, N and K, with a bias and an activation in the epilogue
+# (int8: the column-sum correction and fused dequantisation). Indices follow the
+# configuration tables of gemm_mfma.hip.
+GEMM_CFGS = {"f32": range(4), "bf16": range(6), "bf16x2": range(3), "i8": range(4)}
+
+
+@pytest.mark.parametrize("kind,cfg", [(k, c) for k, r in GEMM_CFGS.items() for c in r])
+@pytest.mark.parametrize("m,n,k", [(70, 197, 300), (257, 100, 1030)])
+def test_gemm_forced_tile_configs(sess, monkeypatch, kind, cfg, m, n, k):
+    announce(f"gemm forced tile kind={kind} cfg={cfg} m={m} n={n} k={k}")
+    monkeypatch.setenv("INGOT_GEMM_CFG", str(cfg))
+    rng = np.random.default_rng(cfg * 1009 + m * 7 + n + k)
+    if kind == "i8":
+        a = rng.integers(0, 256, (m, k)).astype(np.uint8)
+        b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+        sc = rng.uniform(0.001, 0.01, n).astype(np.float32)
+        w = sess.upload_weight(b, trans=False, pack_dtype=L.DT_I8)
+        yi, yf = sess.empty(L.DT_I32, (m, n)), sess.empty(L.DT_F32, (m, n))
+        sess.matmul_integer(sess.to_device(a, L.DT_U8), w, m, 131, y_i32=yi, scale=sess.to_device(sc), y_f32=yf)
+        want = oracle.matmul_integer(a, b, 131)
+        assert np.array_equal(yi.numpy(), want), f"int8 cfg {cfg}"
+        assert np.array_equal(yf.numpy(), oracle.dequantize_linear(want, sc, inner=1)), f"int8 dequant cfg {cfg}"
+        w.free()
+        return
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    if kind == "f32":
+        bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+        w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_F32)
+        wide, kw, bdt = bt, {}, None
+    else:
+        bt = bf16_weights(rng, (n, k))
+        w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+        wide, bdt = oracle.bf16_to_f32(bt), oracle.BF16
+        kw = {"math": L.MATH_BF16} if kind == "bf16" else {}
+    ain = oracle.bf16_to_f32(oracle.f32_to_bf16(a)) if kind == "bf16" else a
+    y = sess.empty(L.DT_F32, (m, n))
+    sess.gemm(sess.to_device(a), w, y, m, beta=1.0, c=sess.to_device(bias), c_mode=L.C_ROW, act=L.ACT_GELU_ERF, **kw)
+    want = oracle.gemm(np.ascontiguousarray(ain), bt, trans_b=True, c=bias, c_mode=L.C_ROW, beta=1.0,
+                       act_code=L.ACT_GELU_ERF, **({"b_dtype": bdt} if bdt is not None else {}))
+    assert_close(y.numpy(), want, nstar_tol(k, a, wide), f"{kind} cfg {cfg}")
+    w.free()
+
+
 @pytest.mark.parametrize("cfg", ["10", "11", "12", "13", "14", "15", "16", "17", "18", "19", "20",
                                  "1", "2", "3", "4", "5", "6", "7"])
 @pytest.mark.parametrize("m", [1, 2, 4, 9, 16])
