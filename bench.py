@@ -102,10 +102,12 @@ class Dit:
             self.y.append(sess.empty(L.DT_F32, (self.M, n)))
             self.acts.append(L.ACT_GELU_ERF if tag.endswith("gelu") else L.ACT_NONE)
         self.flops = sum(2.0 * self.M * n * k for k, n, _ in self.shapes)
+        self.calls = [sess.prepare_gemm(self.a[k], w, y, self.M, act=act, math=L.MATH_BF16)
+                      for (k, n, _), w, y, act in zip(self.shapes, self.w, self.y, self.acts)]
 
     def step(self):
-        for (k, n, _), w, y, act in zip(self.shapes, self.w, self.y, self.acts):
-            self.sess.gemm(self.a[k], w, y, self.M, act=act, math=self.L.MATH_BF16)
+        for call in self.calls:
+            call()
 
     def kernel_roofline(self):
         """The bf16 MFMA GEMM kernel alone: activations already bf16 (one launch per Gemm)."""
@@ -115,9 +117,12 @@ class Dit:
             a16[k] = s.empty(L.DT_BF16, (self.M, k))
             s.cast_bf16(t, a16[k])
 
+        calls = [s.prepare_gemm(a16[k], w, y, self.M, act=act, a_dtype=L.DT_BF16)
+                 for (k, n, _), w, y, act in zip(self.shapes, self.w, self.y, self.acts)]
+
         def launches():
-            for (k, n, _), w, y, act in zip(self.shapes, self.w, self.y, self.acts):
-                s.gemm(a16[k], w, y, self.M, act=act, a_dtype=L.DT_BF16)
+            for call in calls:
+                call()
 
         ms = event_ms(s, launches, 10) / len(self.shapes)
         flops = self.flops / len(self.shapes)
@@ -188,12 +193,13 @@ class Bert:
             self.b.append(sess.to_device(rng.normal(0, 0.02, n).astype(np.float32)))
             self.y.append(sess.empty(L.DT_F32, (self.M, n)))
         self.flops = sum(2.0 * self.M * n * k for k, n, _ in self.shapes)
+        self.calls = [sess.prepare_gemm(self.a[k], w, y, self.M, beta=1.0, c=b, c_mode=L.C_ROW,
+                                        act=L.ACT_GELU_ERF if gelu else L.ACT_NONE)
+                      for (k, n, gelu), w, b, y in zip(self.shapes, self.w, self.b, self.y)]
 
     def step(self):
-        L = self.L
-        for (k, n, gelu), w, b, y in zip(self.shapes, self.w, self.b, self.y):
-            self.sess.gemm(self.a[k], w, y, self.M, beta=1.0, c=b, c_mode=L.C_ROW,
-                           act=L.ACT_GELU_ERF if gelu else L.ACT_NONE)
+        for call in self.calls:
+            call()
 
     def report(self, ms):
         v = self.flops / (ms * 1e-3) / 1e12
@@ -216,9 +222,10 @@ class Int8:
         self.y = sess.empty(L.DT_F32, (self.M, self.N))
         self.ops = 2.0 * self.M * self.N * self.K
         self.bytes = self.M * self.K + self.K * self.N + 4 * self.M * self.N
+        self.call = sess.prepare_matmul_integer(self.a, self.w, self.M, 128, scale=self.scale, y_f32=self.y)
 
     def step(self):
-        self.sess.matmul_integer(self.a, self.w, self.M, 128, scale=self.scale, y_f32=self.y)
+        self.call()
 
     def report(self, ms):
         tops = self.ops / (ms * 1e-3) / 1e12
@@ -242,16 +249,19 @@ class Decode:
         self.y = [sess.empty(L.DT_F32, (16, n)) for _, n in self.shapes]
         self.i = 0
         self.wbytes = sum(2.0 * n * k for k, n in self.shapes)
+        # prepared calls per (M, weight copy): argument blocks built once
+        self.calls = {M: [[sess.prepare_gemm(self.x[k], w, y, M) for (k, n), w, y in zip(self.shapes, ws, self.y)]
+                          for ws in self.w] for M in (1, 4, 16)}
 
     def bytes_step(self, M):
         return self.wbytes + sum(4.0 * M * (k + n) for k, n in self.shapes)
 
     def step(self, M=None):
         M = M or self.M
-        ws = self.w[self.i % self.copies]
+        calls = self.calls[M][self.i % self.copies]
         self.i += 1
-        for (k, n), w, y in zip(self.shapes, ws, self.y):
-            self.sess.gemm(self.x[k], w, y, M)
+        for call in calls:
+            call()
 
     def report(self):
         out = {}
@@ -263,9 +273,9 @@ class Decode:
         # per-shape kernel time at M=1 (events over rotated launches)
         per = {}
         for j, (k, n) in enumerate(self.shapes):
-            def launches(j=j, k=k):
+            def launches(j=j):
                 for c in range(self.copies):
-                    self.sess.gemm(self.x[k], self.w[c][j], self.y[j], 1)
+                    self.calls[1][c][j]()
             ms = event_ms(self.sess, launches, 20) / self.copies
             b = 2.0 * n * k + 4.0 * (k + n)
             per[f"{k}x{n}"] = {"us": round(ms * 1e3, 2), "GB_per_s": round(b / (ms * 1e-3) / 1e9, 1)}
@@ -276,11 +286,14 @@ class Decode:
                                        pack_dtype=L.PACK_I8G) for k, n in self.shapes] for c in range(self.copies)]
         i = [0]
 
+        qcalls = [[self.sess.prepare_gemm(self.x[k], w, y, 1) for (k, n), w, y in zip(self.shapes, ws, self.y)]
+                  for ws in wq]
+
         def step_i8g():
-            ws = wq[i[0] % self.copies]
+            calls = qcalls[i[0] % self.copies]
             i[0] += 1
-            for (k, n), w, y in zip(self.shapes, ws, self.y):
-                self.sess.gemm(self.x[k], w, y, 1)
+            for call in calls:
+                call()
         ms = time_steps(self.sess, step_i8g, 60, 10)
         qbytes = sum(n * k + 4.0 * n * k / 64 + 4.0 * (k + n) for k, n in self.shapes)
         out["m1_i8g"] = {"GB_per_s": round(qbytes / (ms * 1e-3) / 1e9, 1), "us_per_step": round(ms * 1e3, 2),

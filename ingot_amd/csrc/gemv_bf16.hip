@@ -129,8 +129,9 @@ __global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemvArgs p) {
 // fixed butterfly (deterministic). x stays f32 (the reference's f32 dot),
 // except under INGOT_MATH_BF16 (split = 0), where it is rounded to bf16 once.
 // CHX > 0 sets the chunks in flight per step (0: 4, or 2 for MM >= 4).
-template <int R, int MM, int WPB, int CHX = 0>
-__global__ __launch_bounds__(64 * WPB) void gemv_rows_kernel(GemvArgs p) {
+// A is GemvArgs, or PlainView (below) over the 40-byte GemvPlainArgs.
+template <int R, int MM, int WPB, int CHX = 0, typename A = GemvArgs>
+__global__ __launch_bounds__(64 * WPB) void gemv_rows_kernel(A p) {
     constexpr int CH = CHX ? CHX : (MM >= 4 ? 2 : 4);  // chunks in flight per step
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -214,11 +215,43 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows_kernel(GemvArgs p) {
     }
 }
 
-template <int R, int MM, int WPB = 4, int CHX = 0>
-hipError_t launch_rows(const GemvArgs& a, hipStream_t st) {
+template <int R, int MM, int WPB = 4, int CHX = 0, typename A = GemvArgs>
+hipError_t launch_rows(const A& a, hipStream_t st) {
     const int waves = (a.N + R - 1) / R;
-    hipLaunchKernelGGL((gemv_rows_kernel<R, MM, WPB, CHX>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, st, a);
+    hipLaunchKernelGGL((gemv_rows_kernel<R, MM, WPB, CHX, A>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, st, a);
     return hipGetLastError();
+}
+
+// GemvPlainArgs seen through the members gemv_rows_kernel reads: the fixed
+// parts of the plain case are compile-time constants, and its epilogue is the
+// identity with an f32 store.
+struct PlainEpi {};
+__device__ __forceinline__ float epi_apply(const PlainEpi&, float acc, int64_t, int64_t) { return acc; }
+__device__ __forceinline__ void store_y(void* y, int64_t i, float v, const PlainEpi&) { ((float*)y)[i] = v; }
+struct PlainView : GemvPlainArgs {
+    static constexpr int64_t ldx = 0, ldy = 0;
+    static constexpr int M = 1, x_vec = 1, split = 1;
+    PlainEpi epi;
+};
+
+bool gemv_plain_ok(const GemvArgs& a) {
+    const Epi& e = a.epi;
+    return a.M == 1 && a.x_vec && a.split && e.alpha == 1.f && e.c_mode == INGOT_C_NONE && e.act == INGOT_ACT_NONE &&
+           !e.post && !e.y_bf16 && a.ldw <= INT32_MAX && a.kp <= INT32_MAX;
+}
+
+hipError_t launch_gemv_plain(const GemvArgs& a, hipStream_t st) {
+    if (!gemv_plain_ok(a) || a.kp % KR != 0) return hipErrorInvalidValue;
+    PlainView v = {};
+    v.x = a.x;
+    v.w = a.w;
+    v.y = a.y;
+    v.ldw = (int32_t)a.ldw;
+    v.kp = (int32_t)a.kp;
+    v.N = a.N;
+    v.K = a.K;
+    const int64_t chunks = (a.kp + 511) / 512;
+    return chunks > 4 && chunks <= 12 ? launch_rows<1, 1, 4, 12, PlainView>(v, st) : launch_rows<1, 1, 4, 0, PlainView>(v, st);
 }
 
 hipError_t launch_pack_x(const float* x, int64_t ldx, int M, int K, int64_t kp, int split, uint16_t* dst,

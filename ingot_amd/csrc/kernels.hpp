@@ -70,6 +70,18 @@ struct GemvArgs {
 };
 // cfg selects (waves per workgroup, 16-byte chunks per lane per round).
 hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st);
+// The common decode case in a 40-byte argument block (the host cost of a
+// launch grows with the argument size): M = 1, f32 x 16-byte aligned, f32-class
+// math (split), y = x·Wᵀ stored as f32 with no epilogue. The caller checks
+// gemv_plain_ok.
+struct GemvPlainArgs {
+    const float* x;
+    const uint16_t* w;
+    void* y;
+    int32_t ldw, kp, N, K;
+};
+bool gemv_plain_ok(const GemvArgs& a);
+hipError_t launch_gemv_plain(const GemvArgs& a, hipStream_t st);
 // x (f32 [M <= 16][ldx]) → the fragment-ordered bf16 planes the M > 4 GEMV
 // reads: dst holds (split ? 2 : 1) planes of 16·kp elements.
 hipError_t launch_pack_x(const float* x, int64_t ldx, int M, int K, int64_t kp, int split, uint16_t* dst,

@@ -453,7 +453,7 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const 
     }
     int cfg = 0;
     if (const char* f = getenv("INGOT_GEMV_CFG")) cfg = atoi(f);
-    hipError_t e = launch_gemv_bf16(g, cfg, s->stream);
+    hipError_t e = cfg == 0 && gemv_plain_ok(g) ? launch_gemv_plain(g, s->stream) : launch_gemv_bf16(g, cfg, s->stream);
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return INGOT_OK;
 }

@@ -208,6 +208,18 @@ class Session:
         g = self.gemm_args(a, w, y, M, **kw)
         L.check(self.lib.ingot_rocm_gemm(self.h, C.byref(g)))
 
+    def prepare_gemm(self, a: DeviceTensor, w: Weight, y: DeviceTensor, M: int, **kw):
+        """ingot_rocm_gemm with its argument block built once: a callable that
+        enqueues the same product again (what a compiled session does per node)."""
+        ref = C.byref(self.gemm_args(a, w, y, M, **kw))
+        fn, h = self.lib.ingot_rocm_gemm, self.h
+
+        def call() -> None:
+            rc = fn(h, ref)
+            if rc:
+                L.check(rc)
+        return call
+
     def gemm_dynamic_b(self, a: DeviceTensor, b: DeviceTensor, y: DeviceTensor, M: int, N: int, K: int,
                        trans_b: bool, ldb: int, stride_b: int, **kw) -> None:
         """Batched GEMM with a per-item activation B (ingot_rocm_gemm_dynamic_b)."""
@@ -222,10 +234,23 @@ class Session:
     def matmul_integer(self, a: DeviceTensor, w: Weight, M: int, za: int, y_i32: Optional[DeviceTensor] = None,
                        scale: Optional[DeviceTensor] = None, dq_zp: int = 0, y_f32: Optional[DeviceTensor] = None,
                        lda: Optional[int] = None) -> None:
-        L.check(self.lib.ingot_rocm_matmul_integer(
-            self.h, M, w.n, w.k, a.ptr, a.dtype, lda if lda is not None else w.k, za, w.h,
-            y_i32.ptr if y_i32 is not None else None, scale.ptr if scale is not None else None,
-            scale.numel if scale is not None else 1, dq_zp, y_f32.ptr if y_f32 is not None else None))
+        self.prepare_matmul_integer(a, w, M, za, y_i32, scale, dq_zp, y_f32, lda)()
+
+    def prepare_matmul_integer(self, a: DeviceTensor, w: Weight, M: int, za: int,
+                               y_i32: Optional[DeviceTensor] = None, scale: Optional[DeviceTensor] = None,
+                               dq_zp: int = 0, y_f32: Optional[DeviceTensor] = None, lda: Optional[int] = None):
+        """ingot_rocm_matmul_integer with its arguments converted once (see prepare_gemm)."""
+        fn = self.lib.ingot_rocm_matmul_integer
+        args = [self.h, M, w.n, w.k, a.ptr, a.dtype, lda if lda is not None else w.k, za, w.h,
+                y_i32.ptr if y_i32 is not None else None, scale.ptr if scale is not None else None,
+                scale.numel if scale is not None else 1, dq_zp, y_f32.ptr if y_f32 is not None else None]
+        cargs = [t(v) if v is not None else None for t, v in zip(fn.argtypes, args)]
+
+        def call() -> None:
+            rc = fn(*cargs)
+            if rc:
+                L.check(rc)
+        return call
 
     def qlinear_matmul(self, a: DeviceTensor, w: Weight, M: int, za: int, mult: float, zy: int, y: DeviceTensor,
                        lda: Optional[int] = None) -> None:
