@@ -53,11 +53,23 @@ __global__ void pack_x_kernel(const float* x, int64_t ldx, int M, int K, int64_t
     const int r = l & 15;
     const int64_t k0 = (c >> 6) * 32 + (l >> 4) * 8;
     uint16_t h[8], lo[8];
+    float v[8];
+    const float* src = x + (int64_t)r * ldx + k0;
+    if (r < M && k0 + 8 <= K && (((uintptr_t)src) & 15) == 0) {  // two 16-byte loads
+        const f32x4_t a = *(const f32x4_t*)src, b = *(const f32x4_t*)(src + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = a[e];
+            v[e + 4] = b[e];
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (r < M && k0 + e < K) ? src[e] : 0.f;
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float v = (r < M && k0 + e < K) ? x[(int64_t)r * ldx + k0 + e] : 0.f;
-        h[e] = f32_to_bf16(v);
-        lo[e] = f32_to_bf16(v - bf16_to_f32(h[e]));
+        h[e] = f32_to_bf16(v[e]);
+        lo[e] = f32_to_bf16(v[e] - bf16_to_f32(h[e]));
     }
     i32x4_t o;
     __builtin_memcpy(&o, h, 16);
@@ -280,7 +292,9 @@ hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st) {
         if (a.M == 1) return chunks > 4 && chunks <= 12 ? launch_rows<1, 1, 4, 12>(a, st) : launch_rows<1, 1>(a, st);
         if (a.M == 2) return launch_rows<1, 2>(a, st);
         if (a.M <= 4) return a.N >= 4096 ? launch_rows<2, 4, 1>(a, st) : launch_rows<1, 4>(a, st);
-        return launch_mfma<8, 4, 16>(a, st);
+        // 16 rows per workgroup leave CUs idle below N = 4096 (N = 2048: 128
+        // workgroups); 8 rows with 16 waves splitting K there (measured on MI355X)
+        return a.N > 4096 ? launch_mfma<8, 4, 16>(a, st) : launch_mfma<16, 4, 8>(a, st);
     }
     if (a.M <= 4) {
         switch (cfg) {
