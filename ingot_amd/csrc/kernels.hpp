@@ -70,10 +70,10 @@ struct GemvArgs {
 };
 // cfg selects (waves per workgroup, 16-byte chunks per lane per round).
 hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st);
-// The common decode case in a 40-byte argument block (the host cost of a
-// launch grows with the argument size): M = 1, f32 x 16-byte aligned, f32-class
-// math (split), y = x·Wᵀ stored as f32 with no epilogue. The caller checks
-// gemv_plain_ok.
+// The common decode case in a small argument block (the host cost of a launch
+// grows with the argument size; these 40 bytes launch as 48, against 152 for
+// GemvArgs): M = 1, f32 x 16-byte aligned, f32-class math (split), y = x·Wᵀ
+// stored as f32 with no epilogue. The caller checks gemv_plain_ok.
 struct GemvPlainArgs {
     const float* x;
     const uint16_t* w;
