@@ -89,3 +89,18 @@ def test_version_and_error_without_compute():
     assert lib.ingot_rocm_close(None) == 0
     rc = lib.ingot_rocm_sync(None)
     assert rc == _lib.EINVAL and b"nil session" in lib.ingot_rocm_last_error()
+
+
+def test_header_is_strict_c99(tmp_path):
+    """include/ingot_rocm.h compiles as strict C99 (what cgo and other FFIs include)."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if not gcc:
+        pytest.skip("gcc not available")
+    src = tmp_path / "only_header.c"
+    src.write_text('#include "%s"\nint main(void) { return INGOT_OK; }\n' % HEADER)
+    r = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", "-fsyntax-only", str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
