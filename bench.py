@@ -9,7 +9,8 @@ in HBM, rounded to bf16 on their way in, bf16 weights packed once). `value`
 is step FLOPs / step wall time (TFLOPS).
 
 The other BASELINE configs are measured in the same run and reported under
-"workloads" (skip with --no-extra): BERT-base f32 projections,
+"workloads" (skip with --no-extra): the reference's Gemm+ReLU case,
+BERT-base f32 projections,
 int8 MatMulInteger + DequantizeLinear and decode GEMV M=1/4/16
 (configs[3], weights rotated over 3 copies so HBM, not the 256 MB Infinity
 Cache, serves them).
@@ -175,6 +176,34 @@ class Dit:
         return {"value": round(flops * reps / el / 1e12, 4), "unit": "TFLOPS", "cores": threads, "kind": "port",
                 "sample": f"the 3 DiT GEMMs on {rows} of 4096 rows (bf16 weights widened per panel, f32 A), "
                           f"{reps} reps in {el:.1f} s"}
+
+
+class GemmRelu:
+    """BASELINE configs[0], the reference's own CPU-runnable case: one ONNX Gemm, Y = ReLU(A·Bᵀ + bias), f32,
+    A [128,256] ~U(-1,1), B [512,256] ~U(-1,1) (transB = 1), bias [512] ~N(0,0.1), ReLU fused into the store.
+    33.6 MFLOP per call: launch-bound, so also reported as µs per call (HIP events, back-to-back calls)."""
+    name = "gemm_relu"
+
+    def __init__(self, sess, L):
+        rng = np.random.default_rng(7)
+        self.sess = sess
+        self.M, self.K, self.N = 128, 256, 512
+        a = sess.to_device(rng.uniform(-1, 1, (self.M, self.K)).astype(np.float32))
+        self.w = sess.upload_weight(rng.uniform(-1, 1, (self.N, self.K)).astype(np.float32), trans=True,
+                                    pack_dtype=L.DT_F32)
+        b = sess.to_device(rng.normal(0, 0.1, self.N).astype(np.float32))
+        self.y = sess.empty(L.DT_F32, (self.M, self.N))
+        self.keep = (a, b)
+        self.call = sess.prepare_gemm(a, self.w, self.y, self.M, beta=1.0, c=b, c_mode=L.C_ROW, act=L.ACT_RELU)
+        self.flops = 2.0 * self.M * self.N * self.K
+
+    def step(self):
+        self.call()
+
+    def report(self, ms):
+        us = event_ms(self.sess, self.call, 200) * 1e3
+        return {"value": round(self.flops / (us * 1e-6) / 1e12, 3), "unit": "TFLOPS", "us_per_call": round(us, 2),
+                "ms_per_step": round(ms, 4), "dtype": "f32"}
 
 
 class Bert:
@@ -408,7 +437,7 @@ def main() -> int:
                         "dtype": rep["dtype"], "config": {"workload": args.workload}, "detail": rep})
     if args.workload == "dit" and not args.no_extra:
         extra = {}
-        for cls in (Bert, Int8):
+        for cls in (GemmRelu, Bert, Int8):
             log(f"{cls.name}: measuring")
             w = cls(sess, L)
             extra[cls.name] = w.report(time_steps(sess, w.step, 50, 10))

@@ -142,8 +142,11 @@ __device__ __forceinline__ void interleave() {
 // land on 16 distinct 16-byte bank groups of a 256-byte bank line.
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
+template <int KD> struct KernelArgs { typedef GemmArgsF type; };
+template <> struct KernelArgs<KIND_I8> { typedef GemmArgsQ type; };
+
 template <int KD, int BM, int BN, int WGM, int WGN, int NS>
-__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(typename KernelArgs<KD>::type p) {
     constexpr bool SPLIT = KD == KIND_BF16X2;
     constexpr int AP = SPLIT ? 2 : 1;  // activation planes
     constexpr int NW = WGM * WGN;      // waves per workgroup
@@ -316,8 +319,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
                 r0 = __float_as_uint(e.c[e.c_mode == INGOT_C_ROW ? nn : 0]);
         }
     }
-    if (KD != KIND_I8 && tid < EROWS && p.epi.c_mode == INGOT_C_COL)
-        r1 = __float_as_uint(p.epi.c[min(m0 + tid, p.M - 1)]);
+    if constexpr (KD != KIND_I8) {
+        if (tid < EROWS && p.epi.c_mode == INGOT_C_COL) r1 = __float_as_uint(p.epi.c[min(m0 + tid, p.M - 1)]);
+    }
 #pragma unroll
     for (int s = 1; s < NS; ++s) dma(lds + s * SSTRIDE, s);
     if (tid < BN) {
@@ -331,8 +335,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
                                                                                       : -0.0f);
         }
     }
-    if (KD != KIND_I8 && tid < EROWS)
-        ep_row[tid] = p.epi.c_mode == INGOT_C_COL ? p.epi.beta * __uint_as_float(r1) : -0.0f;
+    if constexpr (KD != KIND_I8) {
+        if (tid < EROWS) ep_row[tid] = p.epi.c_mode == INGOT_C_COL ? p.epi.beta * __uint_as_float(r1) : -0.0f;
+    } else {
+        if (tid < EROWS) ep_row[tid] = -0.0f;
+    }
     wait_dma_groups<G, NS>(NS - 1);
     kloop_barrier();  // k-tile 0 in LDS; epilogue terms staged
     read_frags(lds, 0, fa0, fb0);
@@ -371,13 +378,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(GemmArgs p) {
     const int64_t ybatch = (int64_t)blockIdx.y * p.stride_y;
     // 16-byte stores need an aligned row start (n is always a multiple of 4 here)
     uintptr_t ybase;
-    if (KD == KIND_I8)
+    bool y16;  // bf16 output: 8-byte stores (else 16-byte)
+    if constexpr (KD == KIND_I8) {
         ybase = (uintptr_t)(p.qepi.yi ? p.qepi.yi + ybatch : nullptr) | (uintptr_t)(p.qepi.yf ? p.qepi.yf + ybatch : nullptr) |
                 (uintptr_t)(p.qepi.yq ? (uint8_t*)p.qepi.yq + ybatch : nullptr);
-    else
+        y16 = false;
+    } else {
         ybase = (uintptr_t)p.y + ybatch * (p.epi.y_bf16 ? 2 : 4);
-    // f32: 16-byte stores; bf16: 8-byte stores
-    const bool vec_ok = (ybase & (KD != KIND_I8 && p.epi.y_bf16 ? 7 : 15)) == 0 && (p.ldy & 3) == 0;
+        y16 = p.epi.y_bf16;
+    }
+    const bool vec_ok = (ybase & (y16 ? 7 : 15)) == 0 && (p.ldy & 3) == 0;
 
     if constexpr (KD == KIND_I8) {
         const QEpi& q = p.qepi;
@@ -528,7 +538,13 @@ const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 
 template <int KD, int BM, int BN, int WGM, int WGN, int NS>
 hipError_t launch_one(const GemmArgs& a, int batch, hipStream_t st) {
     dim3 grid(a.tiles_m * a.tiles_n, batch);
-    hipLaunchKernelGGL((gemm_kernel<KD, BM, BN, WGM, WGN, NS>), grid, dim3(64 * WGM * WGN), 0, st, a);
+    typename KernelArgs<KD>::type k;
+    static_cast<GemmCore&>(k) = a;
+    if constexpr (KD == KIND_I8)
+        k.qepi = a.qepi;
+    else
+        k.epi = a.epi;
+    hipLaunchKernelGGL((gemm_kernel<KD, BM, BN, WGM, WGN, NS>), grid, dim3(64 * WGM * WGN), 0, st, k);
     return hipGetLastError();
 }
 

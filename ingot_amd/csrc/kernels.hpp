@@ -18,7 +18,8 @@ enum GemmKind { KIND_BF16 = 0, KIND_F32 = 1, KIND_I8 = 2, KIND_BF16X2 = 3, KIND_
 // 128 int8 elements. Packed operands are zero padded to whole k-tiles.
 constexpr int KTILE_BYTES = 128;
 
-struct GemmArgs {
+// The operand and tile description every GEMM launch shares.
+struct GemmCore {
     const char* a;       // A rows [M][...] (row pitch lda_bytes), k-contiguous
     int64_t lda_bytes;
     const char* b;       // packed weight [b_rows][...] (row pitch ldb_bytes)
@@ -36,7 +37,19 @@ struct GemmArgs {
     uint32_t b_bytes;        // extent of the packed weight
     void* y;
     int64_t ldy;
+};
+
+// What the host fills; a launch passes the kernel only the epilogue its kind
+// reads (GemmArgsF or GemmArgsQ): the host cost of a launch grows with the
+// size of its arguments.
+struct GemmArgs : GemmCore {
     Epi epi;
+    QEpi qepi;
+};
+struct GemmArgsF : GemmCore {
+    Epi epi;
+};
+struct GemmArgsQ : GemmCore {
     QEpi qepi;
 };
 
