@@ -314,3 +314,22 @@ def test_dequantize_per_axis_matches_numpy_f32():
     sc = rng.uniform(0.001, 0.01, 5).astype(np.float32)
     want = (x.astype(np.float32) * sc[None, :, None]).astype(np.float32)
     assert np.array_equal(oracle.dequantize_linear(x, sc, inner=4), want)
+
+
+def test_bf16_widening_and_scalar_rounding_agree():
+    """orc_bf16_to_f32 is the exact widening (bits << 16, every pattern incl. NaN
+    payloads and subnormals); the scalar orc_f32_to_bf16 equals the elementwise
+    orc_f32_to_bf16_n the tests above pin."""
+    lib = oracle.lib()
+    hs = np.arange(0, 1 << 16, 97, dtype=np.uint32)
+    for h in hs:
+        got = np.float32(lib.orc_bf16_to_f32(int(h))).view(np.uint32)
+        want = np.uint32(h) << np.uint32(16)
+        if np.isnan(np.uint32(want).view(np.float32)):
+            assert np.isnan(np.uint32(got).view(np.float32)), hex(int(h))
+        else:
+            assert got == want, hex(int(h))
+    rng = np.random.default_rng(11)
+    xs = rng.normal(0, 1e3, 257).astype(np.float32)
+    vec = oracle.f32_to_bf16(xs)
+    assert all(int(lib.orc_f32_to_bf16(float(x))) == int(v) for x, v in zip(xs, vec))
