@@ -291,7 +291,14 @@ hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st) {
         const int64_t chunks = (a.kp + 511) / 512;
         if (a.M == 1) return chunks > 4 && chunks <= 12 ? launch_rows<1, 1, 4, 12>(a, st) : launch_rows<1, 1>(a, st);
         if (a.M == 2) return launch_rows<1, 2>(a, st);
-        if (a.M <= 4) return a.N >= 4096 ? launch_rows<2, 4, 1>(a, st) : launch_rows<1, 4>(a, st);
+        // M = 3..4: one chunk in flight per step keeps these kernels at 46–54
+        // VGPRs (8+ waves per SIMD: the 5632 waves of N = 11264 fit in one
+        // round instead of 1.1 at 95 VGPRs); on MI355X the gate+up GEMV went from
+        // 14.1 to 12.8 µs, QKV 10.1 to 9.4, the 5632-long down rows 11.0 to 10.4.
+        // Short rows at N < 4096 keep two chunks per step (O: 5.7 µs, 5.9 with one).
+        if (a.M <= 4)
+            return a.N >= 4096 ? launch_rows<2, 4, 1, 1>(a, st)
+                               : (a.kp > 4096 ? launch_rows<1, 4, 4, 1>(a, st) : launch_rows<1, 4>(a, st));
         // 16 rows per workgroup leave CUs idle below N = 4096 (N = 2048: 128
         // workgroups); 8 rows with 16 waves splitting K there (measured on MI355X)
         return a.N > 4096 ? launch_mfma<8, 4, 16>(a, st) : launch_mfma<16, 4, 8>(a, st);
@@ -309,6 +316,8 @@ hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st) {
             case 18: return launch_rows<4, 4, 2>(a, st);
             case 19: return launch_rows<2, 2, 1>(a, st);
             case 20: return launch_rows<1, 1, 4, 12>(a, st);
+            case 21: return launch_rows<2, 4, 1, 1>(a, st);
+            case 22: return launch_rows<1, 4, 4, 1>(a, st);
         }
         return hipErrorInvalidValue;
     }

@@ -340,14 +340,14 @@ def test_gemm_forced_tile_configs(sess, monkeypatch, kind, cfg, m, n, k):
     w.free()
 
 
-@pytest.mark.parametrize("cfg", ["10", "11", "12", "13", "14", "15", "16", "17", "18", "19", "20",
+@pytest.mark.parametrize("cfg", ["10", "11", "12", "13", "14", "15", "16", "17", "18", "19", "20", "21", "22",
                                  "1", "2", "3", "4", "5", "6", "7"])
 @pytest.mark.parametrize("m", [1, 2, 4, 9, 16])
 def test_gemv_forced_configs(sess, monkeypatch, cfg, m):
     """Every GEMV launch configuration (INGOT_GEMV_CFG) that applies to M, strided x, both math modes."""
     rows_cfg = int(cfg) >= 10
     mm = {"10": 1, "11": 1, "12": 1, "13": 4, "14": 4, "15": 2, "16": 4, "17": 4, "18": 4, "19": 2,
-          "20": 1}.get(cfg, 16)
+          "20": 1, "21": 4, "22": 4}.get(cfg, 16)
     if (m > 4) == rows_cfg or m > mm:
         pytest.skip("configuration does not cover this M")
     announce(f"gemv cfg={cfg} m={m}")
