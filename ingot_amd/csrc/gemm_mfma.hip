@@ -533,7 +533,11 @@ const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128
 // N = 768 gives exactly 256 tiles), slightly slower on ties, so weighted 0.97.
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}, {32, 96, 4, 0.97f}};
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}};
-const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f}};
+// int8 64×96: two tiles per CU at M = 1024, N = 3072 (512 tiles) instead of three 64×64 ones:
+// 9.0 vs 9.6 µs on MI355X (fewer panel re-reads through L2); 128×96, 32×96, 64×128,
+// 64×192 and deeper rings were slower there.
+const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f},
+                              {64, 96, 3, 1.06f}};
 
 template <int KD, int BM, int BN, int WGM, int WGN, int NS>
 hipError_t launch_one(const GemmArgs& a, int batch, hipStream_t st) {
@@ -593,6 +597,7 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 1: return launch_one<KIND_I8, 128, 128, 2, 2, 2>(a, batch, st);
                 case 2: return launch_one<KIND_I8, 128, 64, 2, 2, 2>(a, batch, st);
                 case 3: return launch_one<KIND_I8, 64, 64, 2, 2, 2>(a, batch, st);
+                case 4: return launch_one<KIND_I8, 64, 96, 2, 2, 2>(a, batch, st);
             }
             break;
     }
