@@ -299,13 +299,16 @@ class Decode:
             gbs = self.bytes_step(M) / (ms * 1e-3) / 1e9
             out[f"m{M}"] = {"GB_per_s": round(gbs, 1), "us_per_step": round(ms * 1e3, 2),
                             "hbm_frac": round(gbs / PEAK["hbm"], 4)}
-        # per-shape kernel time at M=1 (events over rotated launches)
+        # per-shape kernel time at M=1 (events over rotated launches), after a
+        # warm-up pass over every shape so the first one timed is not the one
+        # that follows the M=16 leg
         per = {}
+        time_steps(self.sess, lambda: self.step(1), 20, 0)
         for j, (k, n) in enumerate(self.shapes):
             def launches(j=j):
                 for c in range(self.copies):
                     self.calls[1][c][j]()
-            ms = event_ms(self.sess, launches, 20) / self.copies
+            ms = event_ms(self.sess, launches, 50) / self.copies
             b = 2.0 * n * k + 4.0 * (k + n)
             per[f"{k}x{n}"] = {"us": round(ms * 1e3, 2), "GB_per_s": round(b / (ms * 1e-3) / 1e9, 1)}
         out["m1_per_shape"] = per
