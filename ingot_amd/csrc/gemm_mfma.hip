@@ -534,6 +534,7 @@ const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128
                                 {64, 64, 4, 0.65f},   {192, 256, 1, 0.95f}, {64, 96, 3, 0.72f}};
 // f32 32×96: on MI355X 15% faster than 64×64 over the BERT projections (M = 1024;
 // N = 768 gives exactly 256 tiles), slightly slower on ties, so weighted 0.97.
+// 64×96, 64×128, 96×64, 32×128 and 64×192 were no faster on any of them.
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}, {32, 96, 4, 0.97f}};
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}};
 // int8 64×96: two tiles per CU at M = 1024, N = 3072 (512 tiles) instead of three 64×64 ones:
