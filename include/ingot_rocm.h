@@ -182,7 +182,7 @@ int ingot_rocm_weight_info(const ingot_rocm_weight* w, int64_t* n, int64_t* k, i
  *             once (RNE), the GPUBF16 semantics of graph/device.go:20-30, at
  *             half the MFMA work. The accumulation is always f32.
  *   C       : d_c with c_mode INGOT_C_* and ldc (INGOT_C_FULL only).
- * M <= 16 with bf16 weights runs the split-K GEMV kernel. */
+ * M <= 16 with bf16 weights runs the decode GEMV (ingot_rocm_gemv_bf16). */
 typedef struct ingot_rocm_gemm_args {
     int64_t M, N, K;
     const void* d_a;
@@ -223,8 +223,9 @@ int ingot_rocm_gemm_dynamic_b(ingot_rocm_session* s, const ingot_rocm_gemm_args*
                               int32_t b_dtype, int32_t trans_b, int64_t ldb, int64_t stride_b);
 
 /* Decode GEMV: y[m,n] = alpha·Σ_k x[m,k]·W[n,k] + beta·C (+act) for M <= 16
- * rows of f32 x against a bf16 weight, wavefront split-K with a deterministic
- * reduction (reference: gemvBF16 ops/matmul.go:177-190, GemvBF16
+ * rows of f32 x against a bf16 weight; K is split across the lanes of a wave
+ * (M <= 4) or the waves of a workgroup (M > 4) and the partial sums are added
+ * in a fixed order, so results are run-to-run identical (reference: gemvBF16 ops/matmul.go:177-190, GemvBF16
  * kernels/gemm/bgemm.go:201-206, Metal gemv_bf16 kernels/metal/decode.go:65).
  * Uses the same argument block as ingot_rocm_gemm (a_dtype f32, trans_a 0,
  * batch 1); fails with INGOT_EINVAL for M > 16 or a non-bf16 weight. */

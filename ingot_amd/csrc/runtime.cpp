@@ -4,7 +4,7 @@
 // A session is the ROCm counterpart of the Metal GPUSession's device state
 // (graph/gpu_darwin_arm64.go:96-148): one HIP stream, a size-classed device
 // pool for op outputs (tensor.Pool, tensor/pool.go:10-60), a growable
-// workspace for packed activations and split-K partials, and the table of
+// workspace for packed activations, and the table of
 // packed constant weights (bCache / bf16Packs / bWeights:
 // ops/matmul.go:200-280, ops/quant.go:803-829).
 
@@ -192,9 +192,6 @@ int ingot_rocm_open(int device, ingot_rocm_session** out) {
     e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&s->t0);
     if (e == hipSuccess) e = hipEventCreate(&s->t1);
-    if (e == hipSuccess) e = hipMalloc((void**)&s->counters, sizeof(unsigned) * ingot_rocm_session::kCounters);
-    if (e == hipSuccess) e = launch_fill(s->counters, 0, sizeof(unsigned) * ingot_rocm_session::kCounters, s->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) {
         int rc = hip_fail(e, "session set-up");
         ingot_rocm_close(s);
@@ -216,7 +213,6 @@ int ingot_rocm_close(ingot_rocm_session* s) {
     }
     for (auto& kv : s->buf_class) (void)hipFree(kv.first);
     if (s->ws) (void)hipFree(s->ws);
-    if (s->counters) (void)hipFree(s->counters);
     if (s->t0) (void)hipEventDestroy(s->t0);
     if (s->t1) (void)hipEventDestroy(s->t1);
     if (s->stream) (void)hipStreamDestroy(s->stream);

@@ -20,14 +20,12 @@ struct ingot_rocm_weight {
 };
 
 struct ingot_rocm_session {
-    static constexpr int64_t kCounters = 1 << 16;  // split-K arrival counters
     int device = 0;
     int num_cus = 256;
     hipStream_t stream = nullptr;
     hipEvent_t t0 = nullptr, t1 = nullptr;
-    void* ws = nullptr;  // workspace: packed activations, split-K partials
+    void* ws = nullptr;  // workspace: packed activations (bf16 A planes, GEMV x planes, int8 A, im2col)
     size_t ws_bytes = 0;
-    unsigned* counters = nullptr;
     std::vector<ingot_rocm_weight*> weights;
     std::map<size_t, std::vector<void*>> free_bufs;    // pool: size class → free buffers
     std::unordered_map<void*, size_t> buf_class;       // pool: buffer → size class
