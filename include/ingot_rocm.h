@@ -178,7 +178,9 @@ int ingot_rocm_weight_info(const ingot_rocm_weight* w, int64_t* n, int64_t* k, i
  *   math    : INGOT_MATH_AUTO follows the weight's packed dtype. f32 A with
  *             bf16 weights then runs as two bf16 planes (hi = bf16(a),
  *             lo = bf16(a − hi)), keeping the reference's f32-activation
- *             accuracy (~2⁻¹⁷ relative). INGOT_MATH_BF16 rounds A to bf16
+ *             accuracy (~2⁻¹⁷ relative); ±Inf and NaN in A propagate as in
+ *             the f32 dot, and finite A never overflows to Inf in the split.
+ *             INGOT_MATH_BF16 rounds A to bf16
  *             once (RNE), the GPUBF16 semantics of graph/device.go:20-30, at
  *             half the MFMA work. The accumulation is always f32.
  *   C       : d_c with c_mode INGOT_C_* and ldc (INGOT_C_FULL only).

@@ -28,6 +28,27 @@ __host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return f;
 }
 
+// f32 x as two bf16 terms, hi + lo = x to within 2⁻¹⁷|x|, so that hi·w + lo·w
+// over a bf16 w keeps f32-activation accuracy: hi = bf16(x) (RNE), lo =
+// bf16(x − hi). Two cases keep the products IEEE-faithful: a finite x whose
+// rounding overflows (|x| >= 0x1.ffp127) takes hi = ±0x7F7F, the largest
+// finite bf16, so lo stays finite; a non-finite x (±Inf, NaN) is carried by
+// hi alone with lo = +0, so ±Inf·w is ±Inf (not Inf − Inf = NaN) as in the
+// f32 dot.
+__host__ __device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+    uint32_t b;
+    __builtin_memcpy(&b, &x, 4);
+    uint16_t h = f32_to_bf16(x);
+    if ((b & 0x7FFFFFFFu) >= 0x7F800000u) {
+        hi = h;
+        lo = 0;
+        return;
+    }
+    if ((h & 0x7FFFu) == 0x7F80u) h = (uint16_t)((h & 0x8000u) | 0x7F7Fu);
+    hi = h;
+    lo = f32_to_bf16(x - bf16_to_f32(h));
+}
+
 // Float epilogue: y = post_scale·act(alpha·acc + beta·C) + post_shift.
 // The C operand follows the Gemm broadcast rules of ops/matmul.go:50-76.
 struct Epi {

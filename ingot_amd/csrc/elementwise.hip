@@ -73,7 +73,7 @@ __global__ void colsum_kernel(const int8_t* packed, int64_t kp, int64_t ldk, int
 
 // Packs activations into [m][kl] rows of dst_kind, zero padded beyond k.
 // Each thread produces one 16-byte chunk of a destination row. KIND_BF16X2
-// writes two planes: hi = bf16(a) at dst, lo = bf16(a − hi) at dst + plane.
+// writes two planes, hi at dst and lo at dst + plane (split_bf16).
 __device__ __forceinline__ float load_a(const char* sb, int src_dt, int trans, int64_t lda, int64_t row, int64_t kk) {
     const int64_t si = trans ? kk * lda + row : row * lda + kk;
     return load_f(sb, src_dt, si);
@@ -133,16 +133,18 @@ __global__ void pack_a_kernel(const void* src, int src_dt, int64_t lda, int tran
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = k0 + e < k ? load_a(sb, src_dt, trans, lda, row, k0 + e) : 0.f;
             }
-            uint16_t h[8];
+            uint16_t h[8], l[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = f32_to_bf16(v[e]);
+            for (int e = 0; e < 8; ++e) {
+                if (KD == KIND_BF16X2)
+                    split_bf16(v[e], h[e], l[e]);
+                else
+                    h[e] = f32_to_bf16(v[e]);
+            }
             i32x4_t out;
             __builtin_memcpy(&out, h, 16);
             *(i32x4_t*)db = out;
             if (KD == KIND_BF16X2) {
-                uint16_t l[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) l[e] = f32_to_bf16(v[e] - bf16_to_f32(h[e]));
                 __builtin_memcpy(&out, l, 16);
                 *(i32x4_t*)(db + plane * esz_d) = out;
             }

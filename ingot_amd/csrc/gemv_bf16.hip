@@ -9,7 +9,8 @@
 // operand (RB weight rows, the rest of the 16 zero) and the activations as
 // the second (16 rows, zero beyond M). To keep f32 activation accuracy, x is
 // split once per call, before this kernel, into bf16 hi + lo planes
-// (hi = bf16(x), lo = bf16(x − hi); |x − hi − lo| <= 2⁻¹⁷|x|) and both are
+// (split_bf16: hi = bf16(x), lo = bf16(x − hi); |x − hi − lo| <= 2⁻¹⁷|x|;
+// non-finite x in hi alone) and both are
 // multiplied: bf16×bf16 products are exact in f32, so the only roundings are
 // the f32 accumulations, as in the reference's f32 dot
 // (kernels/vek/vek_generic.go:183-190). Under INGOT_MATH_BF16 (split = 0)
@@ -44,7 +45,7 @@ constexpr int KR = 256;  // k granularity of the packed weight
 
 // x (f32 [M][ldx]) → bf16 planes in MFMA fragment order: 16-byte chunk c is
 // step s = c / 64, lane l = c % 64 (row r = l % 16, k = 32s + 8(l / 16));
-// rows >= M and k >= K are zero. hi = bf16(x) RNE; lo = bf16(x − hi).
+// rows >= M and k >= K are zero. split: hi, lo = split_bf16(x); else hi = bf16(x) RNE.
 __global__ void pack_x_kernel(const float* x, int64_t ldx, int M, int K, int64_t chunks, int split, uint16_t* dst,
                               int64_t plane) {
     const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -68,8 +69,10 @@ __global__ void pack_x_kernel(const float* x, int64_t ldx, int M, int K, int64_t
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        h[e] = f32_to_bf16(v[e]);
-        lo[e] = f32_to_bf16(v[e] - bf16_to_f32(h[e]));
+        if (split)
+            split_bf16(v[e], h[e], lo[e]);
+        else
+            h[e] = f32_to_bf16(v[e]);
     }
     i32x4_t o;
     __builtin_memcpy(&o, h, 16);

@@ -372,6 +372,44 @@ def test_gemv_forced_configs(sess, monkeypatch, cfg, m):
     w.free()
 
 
+@pytest.mark.parametrize("m", [1, 4, 9, 37])
+def test_special_activations_follow_ieee(sess, m):
+    """±Inf, NaN and near-f32-max activations against bf16 weights, f32-class math: the row GEMV (M <= 4), the
+    hi/lo MFMA GEMV (M <= 16) and the hi/lo GEMM (M > 16) give the float64 oracle's NaN and ±Inf positions
+    and signs (an Inf activation gives ±Inf as in the reference's f32 dot, not the NaN of Inf − Inf in the lo
+    term; a finite 3.4e38 stays finite, not the Inf of its bf16 rounding), and the finite values agree."""
+    announce(f"special activations m={m}")
+    rng = np.random.default_rng(100 + m)
+    n, k = 96, 512
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    kinds = [r % 5 for r in range(m)]
+    for r, kind in enumerate(kinds):
+        if kind == 0:
+            x[r, 7] = np.inf
+        elif kind == 1:
+            x[r, 3], x[r, 100] = -np.inf, np.inf  # per column ±Inf or NaN, by the two weights' signs
+        elif kind == 2:
+            x[r, 11] = np.nan
+        elif kind == 3:
+            x[r, 5] = 3.4e38
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    y = sess.empty(L.DT_F32, (m, n))
+    sess.gemm(sess.to_device(x), w, y, m)
+    got = y.numpy().astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = np.asarray(oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16), np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), "NaN positions differ"
+    inf = np.isinf(want)
+    assert np.array_equal(np.isinf(got), inf), "Inf positions differ"
+    assert np.array_equal(np.sign(got[inf]), np.sign(want[inf])), "Inf signs differ"
+    assert inf[[r for r, kd in enumerate(kinds) if kd == 0]].all()
+    fin = np.isfinite(want)
+    err = np.abs(got[fin] - want[fin])
+    assert np.all(err <= 1e-5 * np.abs(want[fin]) + 1e-3), f"finite values: max err {err.max():.3e}"
+    w.free()
+
+
 # ---------------- BASELINE configs at full size ----------------
 
 def test_config1_gemm_relu(sess):
