@@ -372,13 +372,15 @@ def test_gemv_forced_configs(sess, monkeypatch, cfg, m):
     w.free()
 
 
+@pytest.mark.parametrize("wdt", ["bf16", "f32"])
 @pytest.mark.parametrize("m", [1, 4, 9, 37])
-def test_special_activations_follow_ieee(sess, m):
-    """±Inf, NaN and near-f32-max activations against bf16 weights, f32-class math: the row GEMV (M <= 4), the
-    hi/lo MFMA GEMV (M <= 16) and the hi/lo GEMM (M > 16) give the float64 oracle's NaN and ±Inf positions
-    and signs (an Inf activation gives ±Inf as in the reference's f32 dot, not the NaN of Inf − Inf in the lo
-    term; a finite 3.4e38 stays finite, not the Inf of its bf16 rounding), and the finite values agree."""
-    announce(f"special activations m={m}")
+def test_special_activations_follow_ieee(sess, m, wdt):
+    """±Inf, NaN and near-f32-max activations, f32-class math. bf16 weights: the row GEMV (M <= 4), the hi/lo
+    MFMA GEMV (M <= 16) and the hi/lo GEMM (M > 16); f32 weights: the f32 MFMA GEMM. All give the float64
+    oracle's NaN and ±Inf positions and signs (an Inf activation gives ±Inf as in the reference's f32 dot,
+    not the NaN of Inf − Inf in a lo term; a finite 3.4e38 stays finite, not the Inf of its bf16 rounding),
+    and the finite values agree."""
+    announce(f"special activations m={m} w={wdt}")
     rng = np.random.default_rng(100 + m)
     n, k = 96, 512
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
@@ -392,13 +394,19 @@ def test_special_activations_follow_ieee(sess, m):
             x[r, 11] = np.nan
         elif kind == 3:
             x[r, 5] = 3.4e38
-    wb = bf16_weights(rng, (n, k), 0.02, "normal")
-    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    if wdt == "bf16":
+        wb = bf16_weights(rng, (n, k), 0.02, "normal")
+        w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+        kw = {"b_dtype": oracle.BF16}
+    else:
+        wb = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+        w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_F32)
+        kw = {}
     y = sess.empty(L.DT_F32, (m, n))
     sess.gemm(sess.to_device(x), w, y, m)
     got = y.numpy().astype(np.float64)
     with np.errstate(invalid="ignore", over="ignore"):
-        want = np.asarray(oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16), np.float64)
+        want = np.asarray(oracle.gemm(x, wb, trans_b=True, **kw), np.float64)
     assert np.array_equal(np.isnan(got), np.isnan(want)), "NaN positions differ"
     inf = np.isinf(want)
     assert np.array_equal(np.isinf(got), inf), "Inf positions differ"
