@@ -285,6 +285,18 @@ class Decode:
     def bytes_step(self, M):
         return self.wbytes + sum(4.0 * M * (k + n) for k, n in self.shapes)
 
+    def probe(self):
+        """One plain copy of PROBE_COPY_BYTES (counter calibration), then one step at M = 1, 4 and 16, each on
+        its own weight copy."""
+        L, s = self.L, self.sess
+        src, dst = s.empty(L.DT_U8, (PROBE_COPY_BYTES,)), s.empty(L.DT_U8, (PROBE_COPY_BYTES,))
+        s.memset(src, 1)
+        s.copy_d2d(dst, src)
+        for c, M in enumerate((1, 4, 16)):
+            for call in self.calls[M][c]:
+                call()
+        s.sync()
+
     def step(self, M=None):
         M = M or self.M
         calls = self.calls[M][self.i % self.copies]
@@ -393,8 +405,9 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="measure only the headline workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--probe", action="store_true",
-                    help="counter probe for rocprofv3 --pmc: one calibration copy + one launch of each DiT GEMM")
+    ap.add_argument("--probe", nargs="?", const="dit", choices=["dit", "decode"],
+                    help="counter probe for rocprofv3 --pmc: one calibration copy, then one launch of each DiT GEMM "
+                         "(dit, the default) or one decode GEMV step at M = 1, 4, 16 (decode)")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU (the path has no multi-GPU component); run with --gpus 1")
@@ -405,7 +418,7 @@ def main() -> int:
 
     sess = Session(0)
     if args.probe:
-        Dit(sess, L).probe()
+        (Dit if args.probe == "dit" else Decode)(sess, L).probe()
         sess.close()
         return 0
     res = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
