@@ -9,7 +9,11 @@
  *     1e-3·sqrt(K)·max|A|·max|B| (and ReLU exact at zero).
  *  2. MatMulInteger, u8 A [33, 200] with zero point 128 against s8 B [200, 70]:
  *     int32 results equal to Σ (a − 128)·b exactly.
- *  3. An error: a K that does not match the weight returns INGOT_EINVAL and
+ *  3. The decode GEMV entry point, ingot_rocm_gemv_bf16, at M = 1 and M = 9
+ *     (x [M, 2048] ~U(-1, 1) against a weight [512, 2048] ~U(-0.05, 0.05)
+ *     packed as bf16 by the library): within 1e-3·sqrt(K)·max|x|·max|w| of
+ *     the double-precision product with the bf16-rounded weight.
+ *  4. An error: a K that does not match the weight returns INGOT_EINVAL and
  *     sets ingot_rocm_last_error. */
 #include <math.h>
 #include <stdint.h>
@@ -149,6 +153,66 @@ static void matmul_integer_case(ingot_rocm_session* s) {
     free(a), free(b), free(y);
 }
 
+/* float32 → bfloat16 → float32, round to nearest even (finite inputs) */
+static double bf16_round(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    b = ((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16) << 16;
+    memcpy(&f, &b, 4);
+    return (double)f;
+}
+
+static void gemv_case(ingot_rocm_session* s, int m_rows) {
+    enum { K = 2048, N = 512 };
+    float* x = malloc(sizeof(float) * m_rows * K);
+    float* w = malloc(sizeof(float) * N * K);
+    float* y = malloc(sizeof(float) * m_rows * N);
+    for (int i = 0; i < m_rows * K; ++i) x[i] = uniform(-1.f, 1.f);
+    for (int i = 0; i < N * K; ++i) w[i] = uniform(-0.05f, 0.05f);
+
+    ingot_rocm_weight* wh = NULL;
+    CHECK(ingot_rocm_weight_upload(s, INGOT_DT_F32, INGOT_DT_BF16, N, K, K, 1, w, &wh));
+    void* d_x = to_device(s, x, sizeof(float) * m_rows * K);
+    void* d_y = NULL;
+    CHECK(ingot_rocm_device_alloc(s, sizeof(float) * m_rows * N, &d_y));
+    ingot_rocm_gemm_args g;
+    memset(&g, 0, sizeof g);
+    g.M = m_rows;
+    g.N = N;
+    g.K = K;
+    g.d_a = d_x;
+    g.a_dtype = INGOT_DT_F32;
+    g.lda = K;
+    g.w = wh;
+    g.alpha = 1.f;
+    g.d_y = (float*)d_y;
+    g.ldy = N;
+    g.batch = 1;
+    CHECK(ingot_rocm_gemv_bf16(s, &g));
+    CHECK(ingot_rocm_sync(s));
+    CHECK(ingot_rocm_memcpy_d2h(s, y, d_y, sizeof(float) * m_rows * N));
+
+    const double tol = 1e-3 * sqrt((double)K) * 0.05;  /* max|x| <= 1, max|w| <= 0.05 */
+    double worst = 0.0;
+    for (int m = 0; m < m_rows; ++m)
+        for (int n = 0; n < N; ++n) {
+            double acc = 0.0;
+            for (int k = 0; k < K; ++k) acc += (double)x[m * K + k] * bf16_round(w[n * K + k]);
+            const double err = fabs((double)y[m * N + n] - acc);
+            if (err > worst) worst = err;
+        }
+    if (worst > tol) {
+        fprintf(stderr, "gemv_bf16 M=%d: max-abs error %.3e (tol %.3e)\n", m_rows, worst, tol);
+        ++failures;
+    } else {
+        printf("gemv_bf16 M=%d 2048->512: max-abs error %.3e (tol %.3e)\n", m_rows, worst, tol);
+    }
+    CHECK(ingot_rocm_weight_free(s, wh));
+    CHECK(ingot_rocm_device_free(s, d_x));
+    CHECK(ingot_rocm_device_free(s, d_y));
+    free(x), free(w), free(y);
+}
+
 static void error_case(ingot_rocm_session* s) {
     float b[4 * 3] = {0};
     ingot_rocm_weight* w = NULL;
@@ -186,6 +250,8 @@ int main(void) {
     CHECK(ingot_rocm_open(0, &s));
     gemm_relu_case(s);
     matmul_integer_case(s);
+    gemv_case(s, 1);
+    gemv_case(s, 9);
     error_case(s);
     CHECK(ingot_rocm_close(s));
     if (failures) {
