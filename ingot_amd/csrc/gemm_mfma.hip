@@ -544,7 +544,7 @@ const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 6
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}};
 // int8 64×96: two tiles per CU at M = 1024, N = 3072 (512 tiles) instead of three 64×64 ones:
 // 9.0 vs 9.6 µs on MI355X (fewer panel re-reads through L2); 128×96, 32×96, 64×128,
-// 64×192 and deeper rings were slower there.
+// 64×192, 32-row tiles (32×32 to 32×128) and deeper rings were slower there.
 const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f},
                               {64, 96, 3, 1.06f}};
 
