@@ -525,13 +525,22 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(typename Kernel
 // Tile configurations per kind. occupancy: workgroups per CU the LDS and
 // register footprint allow; eff: relative throughput per CU slot (measured
 // on MI355X for the bf16 kernel).
-// Small tiles keep two LDS stages: at these sizes occupancy (more resident
-// workgroups) hides latency better than a deeper ring (measured on MI355X).
+// Small tiles mostly keep two LDS stages: with several tiles per CU, occupancy
+// (more resident workgroups) hides latency better than a deeper ring. With one
+// tile per CU or fewer (small M, or few columns) each k-tile waits for its own
+// DMA round trip instead, and a four-stage ring pays: the 32×32 and 64×64
+// four-stage entries (bf16 and bf16 hi/lo), measured on MI355X with bf16
+// weights at K = 2048: M = 17–128 × N = 2048–6144 6.5–6.8 µs with 32×32
+// (10.7–11.3 with two-stage 64×64; the hi/lo kind 11.0 vs 35 with 128×128),
+// M = 64 × N = 11264 and M = 256 × N = 6144 11.1 and 15.4 µs with 64×64
+// (18.1 and 18.5 with two stages). Their weights keep the DiT shapes on the
+// large tiles, and they are taken only when every tile is resident at once.
 // bf16 64×96: at M = 1024, K = 768 (the BERT-size FFN-up and QKV products) two tiles per CU
 // instead of three 64×64 ones: 11.4 vs 12.0–13.1 µs at N = 3072, 10.1 vs 11.5 µs at N = 2304 on
 // MI355X; slower at N = 768 (fewer tiles than CUs), where the weight keeps 64×64 ahead.
 const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128, 128, 2, 0.80f}, {128, 64, 3, 0.78f},
-                                {64, 64, 4, 0.65f},   {192, 256, 1, 0.95f}, {64, 96, 3, 0.72f}};
+                                {64, 64, 4, 0.65f},   {192, 256, 1, 0.95f}, {64, 96, 3, 0.72f}, {32, 32, 4, 0.60f, true},
+                                {64, 64, 2, 1.00f, true}};
 // f32 32×96: on MI355X 15% faster than 64×64 over the BERT projections (M = 1024;
 // N = 768 gives exactly 256 tiles), slightly slower on ties, so weighted 0.97.
 // 64×96, 64×128, 96×64, 32×128 and 64×192 were no faster on any of them.
@@ -541,7 +550,8 @@ const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128
 // 32×96 on the BERT projections, so weighted 0.8.
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}, {32, 96, 4, 0.97f},
                                {32, 32, 8, 0.80f}};
-const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}};
+const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}, {32, 32, 3, 0.60f, true},
+                                  {64, 64, 1, 1.00f, true}};
 // int8 64×96: two tiles per CU at M = 1024, N = 3072 (512 tiles) instead of three 64×64 ones:
 // 9.0 vs 9.6 µs on MI355X (fewer panel re-reads through L2); 128×96, 32×96, 64×128,
 // 64×192, 32-row tiles (32×32 to 32×128) and deeper rings were slower there.
@@ -584,6 +594,8 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 4: return launch_one<KIND_BF16, 64, 64, 2, 2, 2>(a, batch, st);
                 case 5: return launch_one<KIND_BF16, 192, 256, 2, 4, 2>(a, batch, st);
                 case 6: return launch_one<KIND_BF16, 64, 96, 2, 2, 2>(a, batch, st);
+                case 7: return launch_one<KIND_BF16, 32, 32, 2, 2, 4>(a, batch, st);
+                case 8: return launch_one<KIND_BF16, 64, 64, 2, 2, 4>(a, batch, st);
             }
             break;
         case KIND_BF16X2:
@@ -591,6 +603,8 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 0: return launch_one<KIND_BF16X2, 128, 128, 2, 2, 2>(a, batch, st);
                 case 1: return launch_one<KIND_BF16X2, 128, 64, 2, 2, 2>(a, batch, st);
                 case 2: return launch_one<KIND_BF16X2, 64, 64, 2, 2, 2>(a, batch, st);
+                case 3: return launch_one<KIND_BF16X2, 32, 32, 2, 2, 4>(a, batch, st);
+                case 4: return launch_one<KIND_BF16X2, 64, 64, 2, 2, 4>(a, batch, st);
             }
             break;
         case KIND_F32:

@@ -57,6 +57,7 @@ struct GemmConfig {
     int bm, bn;
     int occupancy;   // workgroups per CU the tile allows
     float eff;       // relative per-CU efficiency (tile-size heuristic)
+    bool one_round;  // only when every tile is resident at once (a latency-bound shape)
 };
 
 // Tile configurations compiled for `kind`; index used by launch_gemm.

@@ -45,6 +45,8 @@ int kind_size(GemmKind k) { return k == KIND_F32 ? 4 : (k == KIND_I8 || k == KIN
 
 // Picks the tile configuration with the least estimated time: full rounds of
 // num_cus·occupancy workgroups, each round as long as the most loaded CU.
+// Deep-ring entries marked one_round apply only when a single round holds
+// every tile.
 int pick_config(GemmKind kind, int64_t M, int64_t N, int64_t batch, int num_cus) {
     const char* force = getenv("INGOT_GEMM_CFG");
     const GemmConfig* c;
@@ -59,6 +61,7 @@ int pick_config(GemmKind kind, int64_t M, int64_t N, int64_t batch, int num_cus)
         const int64_t tiles = ((M + c[i].bm - 1) / c[i].bm) * ((N + c[i].bn - 1) / c[i].bn) * batch;
         const int64_t slots = (int64_t)num_cus * c[i].occupancy;
         const int64_t rounds = (tiles + slots - 1) / slots;
+        if (c[i].one_round && rounds > 1) continue;
         const int64_t per_cu = std::min<int64_t>(c[i].occupancy, (tiles + num_cus - 1) / num_cus);
         const double t = (double)rounds * (double)per_cu * c[i].bm * c[i].bn / c[i].eff;
         if (t < best_t * 0.999) {
