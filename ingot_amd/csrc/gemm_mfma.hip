@@ -544,12 +544,13 @@ const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128
 // f32 32×96: on MI355X 15% faster than 64×64 over the BERT projections (M = 1024;
 // N = 768 gives exactly 256 tiles), slightly slower on ties, so weighted 0.97.
 // 64×96, 64×128, 96×64, 32×128 and 64×192 were no faster on any of them.
-// f32 32×32: for products with few tiles. The configs[0] Gemm (M = 128, N = 512,
-// K = 256) runs 64 of them instead of 24 32×96 ones: 3.8 vs 6.2 µs per call on
-// MI355X (a deeper ring, all 8 k-tiles in flight, was slower). 6–12% slower than
-// 32×96 on the BERT projections, so weighted 0.8.
+// f32 32×32, four-stage ring: for products with few tiles. The configs[0] Gemm
+// (M = 128, N = 512, K = 256) runs 64 of them instead of 24 32×96 ones: 3.8 vs
+// 6.2 µs per call on MI355X; at M = 32, N = 6144, K = 2048 (64 k-tiles) the ring
+// depth matters: 14.2 µs with four stages, 26.8 with two. 6–12% slower than 32×96
+// on the BERT projections, so weighted 0.8.
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}, {32, 96, 4, 0.97f},
-                               {32, 32, 8, 0.80f}};
+                               {32, 32, 4, 0.80f}};
 const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}, {32, 32, 3, 0.60f, true},
                                   {64, 64, 1, 1.00f, true}};
 // int8 64×96: two tiles per CU at M = 1024, N = 3072 (512 tiles) instead of three 64×64 ones:
@@ -613,7 +614,7 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 1: return launch_one<KIND_F32, 128, 64, 2, 2, 2>(a, batch, st);
                 case 2: return launch_one<KIND_F32, 64, 64, 2, 2, 2>(a, batch, st);
                 case 3: return launch_one<KIND_F32, 32, 96, 2, 2, 2>(a, batch, st);
-                case 4: return launch_one<KIND_F32, 32, 32, 2, 2, 2>(a, batch, st);
+                case 4: return launch_one<KIND_F32, 32, 32, 2, 2, 4>(a, batch, st);
             }
             break;
         case KIND_I8:
