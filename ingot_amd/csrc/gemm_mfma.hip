@@ -556,8 +556,10 @@ const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64
 // int8 64×96: two tiles per CU at M = 1024, N = 3072 (512 tiles) instead of three 64×64 ones:
 // 9.0 vs 9.6 µs on MI355X (fewer panel re-reads through L2); 128×96, 32×96, 64×128,
 // 64×192, 32-row tiles (32×32 to 32×128) and deeper rings were slower there.
+// int8 32×32 with a four-stage ring, for products whose tiles are all resident
+// at once: M = 1–128 at K = 768–2048 took 3.8–5.3 µs instead of 4.7–6.9.
 const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 64, 3, 0.70f}, {64, 64, 4, 1.00f},
-                              {64, 96, 3, 1.06f}};
+                              {64, 96, 3, 1.06f}, {32, 32, 4, 0.60f, true}};
 
 template <int KD, int BM, int BN, int WGM, int WGN, int NS>
 hipError_t launch_one(const GemmArgs& a, int batch, hipStream_t st) {
@@ -624,6 +626,7 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 2: return launch_one<KIND_I8, 128, 64, 2, 2, 2>(a, batch, st);
                 case 3: return launch_one<KIND_I8, 64, 64, 2, 2, 2>(a, batch, st);
                 case 4: return launch_one<KIND_I8, 64, 96, 2, 2, 2>(a, batch, st);
+                case 5: return launch_one<KIND_I8, 32, 32, 2, 2, 4>(a, batch, st);
             }
             break;
     }
