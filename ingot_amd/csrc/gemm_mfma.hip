@@ -563,6 +563,10 @@ const GemmConfig kI8Cfgs[] = {{256, 256, 1, 1.00f}, {128, 128, 2, 0.60f}, {128, 
 
 template <int KD, int BM, int BN, int WGM, int WGN, int NS>
 hipError_t launch_one(const GemmArgs& a, int batch, hipStream_t st) {
+    // the grid was sized from the configuration table: it must be exactly this tile's
+    if ((int64_t)a.tiles_m * BM < a.M || (int64_t)(a.tiles_m - 1) * BM >= a.M || (int64_t)a.tiles_n * BN < a.N ||
+        (int64_t)(a.tiles_n - 1) * BN >= a.N)
+        return hipErrorInvalidValue;
     dim3 grid(a.tiles_m * a.tiles_n, batch);
     typename KernelArgs<KD>::type k;
     static_cast<GemmCore&>(k) = a;
