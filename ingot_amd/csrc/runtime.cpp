@@ -542,8 +542,12 @@ static int gemm_core(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const
     const int64_t batch = std::max<int64_t>(1, a->batch);
     if (a->M == 0 || a->N == 0) return INGOT_OK;
     if (w->kind == KIND_I8G) return run_gemv_i8g(s, a, w);
-    if (w->kind == KIND_BF16 && a->M <= 16 && !a->trans_a && a->a_dtype == INGOT_DT_F32 && batch == 1 &&
-        !getenv("INGOT_NO_GEMV"))
+    // Decode rows take the GEMV: all of M <= 4, and M = 5..16 for N < 4096. At
+    // M = 5..16 the wider products run faster as a GEMM of four-stage 32×32
+    // tiles (on MI355X at K = 2048, M = 8 and 16: N = 6144 10.7 vs 12.7 µs, N =
+    // 11264 13.1 vs 16.2 µs; N = 2048 the GEMV stays ahead, 8.7 vs 10.4 µs).
+    if (w->kind == KIND_BF16 && a->M <= 16 && (a->M <= 4 || a->N < 4096) && !a->trans_a &&
+        a->a_dtype == INGOT_DT_F32 && batch == 1 && !getenv("INGOT_NO_GEMV"))
         return run_gemv(s, a, w);
 
     // bf16 weights with f32 activations: two bf16 planes (f32-class accuracy)
