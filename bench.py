@@ -230,6 +230,11 @@ class Bert:
         for call in self.calls:
             call()
 
+    def probe(self):
+        """One launch of each BERT projection (for rocprofv3 --pmc)."""
+        self.step()
+        self.sess.sync()
+
     def report(self, ms):
         v = self.flops / (ms * 1e-3) / 1e12
         return {"value": round(v, 2), "unit": "TFLOPS", "ms_per_step": round(ms, 4), "dtype": "f32",
@@ -405,9 +410,10 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="measure only the headline workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--probe", nargs="?", const="dit", choices=["dit", "decode"],
+    ap.add_argument("--probe", nargs="?", const="dit", choices=["dit", "decode", "bert"],
                     help="counter probe for rocprofv3 --pmc: one calibration copy, then one launch of each DiT GEMM "
-                         "(dit, the default) or one decode GEMV step at M = 1, 4, 16 (decode)")
+                         "(dit, the default) or one decode GEMV step at M = 1, 4, 16 (decode); bert: one launch of "
+                         "each BERT f32 projection")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU (the path has no multi-GPU component); run with --gpus 1")
@@ -418,7 +424,7 @@ def main() -> int:
 
     sess = Session(0)
     if args.probe:
-        (Dit if args.probe == "dit" else Decode)(sess, L).probe()
+        {"dit": Dit, "decode": Decode, "bert": Bert}[args.probe](sess, L).probe()
         sess.close()
         return 0
     res = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
