@@ -261,6 +261,15 @@ class Int8:
     def step(self):
         self.call()
 
+    def probe(self):
+        """One plain copy of PROBE_COPY_BYTES (counter calibration), then one MatMulInteger + dequant call."""
+        L, s = self.L, self.sess
+        src, dst = s.empty(L.DT_U8, (PROBE_COPY_BYTES,)), s.empty(L.DT_U8, (PROBE_COPY_BYTES,))
+        s.memset(src, 1)
+        s.copy_d2d(dst, src)
+        self.call()
+        s.sync()
+
     def report(self, ms):
         tops = self.ops / (ms * 1e-3) / 1e12
         gbs = self.bytes / (ms * 1e-3) / 1e9
@@ -410,10 +419,10 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="measure only the headline workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--probe", nargs="?", const="dit", choices=["dit", "decode", "bert"],
+    ap.add_argument("--probe", nargs="?", const="dit", choices=["dit", "decode", "bert", "int8"],
                     help="counter probe for rocprofv3 --pmc: one calibration copy, then one launch of each DiT GEMM "
                          "(dit, the default) or one decode GEMV step at M = 1, 4, 16 (decode); bert: one launch of "
-                         "each BERT f32 projection")
+                         "each BERT f32 projection; int8: one calibration copy, then one MatMulInteger + dequant call")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU (the path has no multi-GPU component); run with --gpus 1")
@@ -424,7 +433,7 @@ def main() -> int:
 
     sess = Session(0)
     if args.probe:
-        {"dit": Dit, "decode": Decode, "bert": Bert}[args.probe](sess, L).probe()
+        {"dit": Dit, "decode": Decode, "bert": Bert, "int8": Int8}[args.probe](sess, L).probe()
         sess.close()
         return 0
     res = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
