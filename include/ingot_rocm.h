@@ -184,7 +184,10 @@ int ingot_rocm_weight_info(const ingot_rocm_weight* w, int64_t* n, int64_t* k, i
  *             once (RNE), the GPUBF16 semantics of graph/device.go:20-30, at
  *             half the MFMA work. The accumulation is always f32.
  *   C       : d_c with c_mode INGOT_C_* and ldc (INGOT_C_FULL only).
- * M <= 16 with bf16 weights runs the decode GEMV (ingot_rocm_gemv_bf16). */
+ * Routing of bf16 weights with f32 A (no transA, batch 1): M <= 4 runs the
+ * decode GEMV of ingot_rocm_gemv_bf16, and so does M = 5..16 when N < 4096;
+ * M = 5..16 with N >= 4096 runs the GEMM (four-stage 32x32 tiles), which is
+ * faster there. ingot_rocm_gemv_bf16 always runs the GEMV (M <= 16). */
 typedef struct ingot_rocm_gemm_args {
     int64_t M, N, K;
     const void* d_a;
@@ -333,6 +336,15 @@ int ingot_rocm_op_create(ingot_rocm_session* s, const char* domain, const char* 
  * from the session pool (ctx.NewUninit). `*n_out` receives the count. */
 int ingot_rocm_op_run(ingot_rocm_op* op, int n_in, const ingot_rocm_tensor* in, int max_out, ingot_rocm_tensor* out,
                       int* n_out);
+/* Declares input `input` of the op constant (is_const = 1): its device storage
+ * holds the same values on every run, as a graph initializer does. Such a
+ * weight operand is packed once and the pack reused; every undeclared operand
+ * is packed per call, since a pooled device buffer is handed back at the same
+ * address with new contents. The reference's GPU session caches only graph
+ * constants, by value id (bf16Const, graph/gpuops_darwin_arm64.go:610-629);
+ * the CPU bCache keys on storage (ops/matmul.go:200-236). The graph session
+ * marks its bound constants itself. */
+int ingot_rocm_op_set_const(ingot_rocm_op* op, int input, int is_const);
 int ingot_rocm_op_free(ingot_rocm_op* op);
 /* Returns an op output's storage to the session pool (Session.Release). */
 int ingot_rocm_tensor_release(ingot_rocm_session* s, ingot_rocm_tensor* t);

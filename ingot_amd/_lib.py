@@ -109,6 +109,7 @@ SIGNATURES = {
                                        C.POINTER(C.c_void_p)]),
     "ingot_rocm_op_run": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(Tensor), C.c_int, C.POINTER(Tensor),
                                     C.POINTER(C.c_int)]),
+    "ingot_rocm_op_set_const": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
     "ingot_rocm_op_free": (C.c_int, [C.c_void_p]),
     "ingot_rocm_tensor_release": (C.c_int, [C.c_void_p, C.POINTER(Tensor)]),
 }

@@ -393,6 +393,11 @@ int ingot_rocm_graph_compile(ingot_rocm_graph* g, int flags) {
         std::string attrs = n.attrs;
         int rc = ingot_rocm_op_create(g->s, n.domain.c_str(), n.op.c_str(), n.opset, attrs.c_str(), &n.impl);
         if (rc) return rc;
+        // bound constants keep their storage and values across runs: the op may
+        // pack them once (every other operand is packed per call)
+        for (size_t k = 0; k < n.in.size(); ++k)
+            if (n.in[k] >= 0 && g->vals[n.in[k]].is_const && (rc = ingot_rocm_op_set_const(n.impl, (int)k, 1)))
+                return rc;
         if (n.fused_act != INGOT_ACT_NONE || n.half || n.half_out) {
             rc = op_plan(n.impl, n.fused_act, n.half, n.half_out);
             if (rc) return fail(rc, "graph: %s does not take a plan", n.op.c_str());

@@ -217,6 +217,14 @@ class Op {
         (void)fused_act, (void)half, (void)out_bf16;
         return INGOT_EDECLINED;
     }
+    // Inputs the caller declared constant (graph constants: their device
+    // storage holds the same values on every run). Only those are packed
+    // once and cached; every other operand is packed per call, since a
+    // pooled device buffer is handed back at the same address with new
+    // contents (the reference's GPU session likewise caches only graph
+    // constants, by value id: bf16Const, graph/gpuops_darwin_arm64.go:610-629).
+    std::vector<char> const_in;
+    bool is_const(size_t i) const { return i < const_in.size() && const_in[i]; }
 };
 
 typedef std::function<int(const NodeInfo&, std::unique_ptr<Op>*)> Builder;
@@ -301,11 +309,12 @@ struct BCache {
     bool dyn = false;
     ingot_rocm_weight* pb = nullptr;
 
-    // Returns the cached pack, or nullptr when the operand is dynamic.
-    int get(ingot_rocm_session* s, const T& b, int trans_, int pack_dtype_, ingot_rocm_weight** out) {
+    // Returns the cached pack, or nullptr when the operand is not a declared
+    // constant or has proven dynamic (the caller packs per call).
+    int get(ingot_rocm_session* s, const T& b, bool constant, int trans_, int pack_dtype_, ingot_rocm_weight** out) {
         std::lock_guard<std::mutex> g(mu);
         *out = nullptr;
-        if (dyn || b.n() == 0) return INGOT_OK;
+        if (!constant || dyn || b.n() == 0) return INGOT_OK;
         if (src == b.data && len == b.n() && trans == trans_ && pack_dtype == pack_dtype_) {
             *out = pb;
             return INGOT_OK;
@@ -439,7 +448,7 @@ class GemmOp : public Op {
                 i8g ? INGOT_PACK_I8G : (b.dtype == INGOT_DT_BF16 || half ? INGOT_DT_BF16 : INGOT_DT_F32);
             // the weight source is [N,K] when transB (rows = b.dim(0))
             ingot_rocm_weight* w = nullptr;
-            rc = (i8g ? cache_i8 : cache).get(s, b, transB ? 1 : 0, pack_dt, &w);
+            rc = (i8g ? cache_i8 : cache).get(s, b, is_const(1), transB ? 1 : 0, pack_dt, &w);
             if (rc) return rc;
             TempWeights tmp(s);
             if (!w) {
@@ -587,7 +596,7 @@ class MatMulOp : public Op {
                 Shape b2 = {bs[0], bs[1]};
                 T bt = b;
                 bt.shape = b2;
-                rc = cache.get(s, bt, 0, pack_dt, &w);
+                rc = cache.get(s, bt, is_const(1), 0, pack_dt, &w);
                 if (rc) return rc;
                 TempWeights tmp(s);
                 if (!w) {
@@ -698,8 +707,10 @@ class MatMulIntegerOp : public Op {
         return INGOT_OK;
     }
 
-    // bWeights (ops/quant.go:801-829): packed once per B storage.
-    int b_weights(const T& b, int64_t k, int64_t nn, ingot_rocm_weight** out) {
+    // bWeights (ops/quant.go:801-829): a declared-constant B is packed once
+    // per storage; any other B is packed per call into `tmp`.
+    int b_weights(const T& b, bool constant, int64_t k, int64_t nn, TempWeights& tmp, ingot_rocm_weight** out) {
+        if (!constant) return tmp.pack(INGOT_DT_I8, INGOT_DT_I8, k, nn, 0, b.data, out);
         std::lock_guard<std::mutex> g(mu);
         if (packed && pack_src == b.data && pack_k == k && pack_n == nn) {
             *out = packed;
@@ -787,7 +798,8 @@ class MatMulIntegerOp : public Op {
                 if (rc) return rc;
             } else {
                 ingot_rocm_weight* w = nullptr;
-                rc = b_weights(b, k, nn, &w);
+                TempWeights tmp(s);
+                rc = b_weights(b, is_const(requant ? 3 : 1), k, nn, tmp, &w);
                 if (rc) return rc;
                 if (requant)
                     rc = ingot_rocm_qlinear_matmul(s, m, nn, k, a.data, a.dtype, k, za, w, mult, zy, ydt, out.data);
@@ -1243,6 +1255,15 @@ int ingot_rocm_op_run(ingot_rocm_op* op, int n_in, const ingot_rocm_tensor* in, 
     }
     for (size_t i = 0; i < outs.size(); ++i) out[i] = outs[i];
     *n_out = (int)outs.size();
+    return INGOT_OK;
+}
+
+int ingot_rocm_op_set_const(ingot_rocm_op* op, int input, int is_const) {
+    if (!op) return fail(INGOT_EINVAL, "nil op");
+    if (input < 0 || input >= 64) return fail(INGOT_EINVAL, "input index %d out of range", input);
+    auto& c = op->op->const_in;
+    if ((int)c.size() <= input) c.resize(input + 1, 0);
+    c[input] = is_const ? 1 : 0;
     return INGOT_OK;
 }
 

@@ -46,15 +46,11 @@ int kind_size(GemmKind k) { return k == KIND_F32 ? 4 : (k == KIND_I8 || k == KIN
 // Picks the tile configuration with the least estimated time: full rounds of
 // num_cus·occupancy workgroups, each round as long as the most loaded CU.
 // Deep-ring entries marked one_round apply only when a single round holds
-// every tile.
-int pick_config(GemmKind kind, int64_t M, int64_t N, int64_t batch, int num_cus) {
-    const char* force = getenv("INGOT_GEMM_CFG");
+// every tile. force >= 0 (INGOT_GEMM_CFG) picks that entry when it exists.
+int pick_config(GemmKind kind, int64_t M, int64_t N, int64_t batch, int num_cus, int force) {
     const GemmConfig* c;
     const int n = gemm_configs(kind, &c);
-    if (force && *force) {
-        const int f = atoi(force);
-        if (f >= 0 && f < n) return f;
-    }
+    if (force >= 0 && force < n) return force;
     int best = 0;
     double best_t = 1e300;
     for (int i = 0; i < n; ++i) {
@@ -192,6 +188,16 @@ int ingot_rocm_open(int device, ingot_rocm_session** out) {
     auto* s = new ingot_rocm_session();
     s->device = device;
     s->num_cus = prop.multiProcessorCount;
+    auto env_int = [](const char* name, int dflt) {
+        const char* v = getenv(name);
+        return v && *v ? atoi(v) : dflt;
+    };
+    s->force_gemm_cfg = env_int("INGOT_GEMM_CFG", -1);
+    s->force_gemv_cfg = env_int("INGOT_GEMV_CFG", 0);
+    const int rows = env_int("INGOT_I8G_ROWS", 0);
+    s->i8g_rows = rows == 1 || rows == 2 || rows == 4 ? rows : 0;
+    s->no_gemv = getenv("INGOT_NO_GEMV") != nullptr;
+    s->qconv_path = env_int("INGOT_QCONV_PATH", 0);
     e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&s->t0);
     if (e == hipSuccess) e = hipEventCreate(&s->t1);
@@ -450,8 +456,7 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const 
         g.xb = (const uint16_t*)ws;
         g.xb_plane = 16 * w->kp;
     }
-    int cfg = 0;
-    if (const char* f = getenv("INGOT_GEMV_CFG")) cfg = atoi(f);
+    const int cfg = s->force_gemv_cfg;
     hipError_t e = cfg == 0 && gemv_plain_ok(g) ? launch_gemv_plain(g, s->stream) : launch_gemv_bf16(g, cfg, s->stream);
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return INGOT_OK;
@@ -489,9 +494,8 @@ static int run_gemv_i8g(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, co
         if (g.epi.c_mode == INGOT_C_COL) g.epi.c += m0;
         g.y = (char*)a->d_y + m0 * a->ldy * (g.epi.y_bf16 ? 2 : 4);
         g.ldy = a->ldy;
-        int cfg = 0;
-        if (const char* f = getenv("INGOT_I8G_ROWS")) cfg = atoi(f);
-        e = launch_gemv_i8g(g, cfg == 1 || cfg == 2 || cfg == 4 ? cfg : 0, s->stream);
+        const int cfg = s->i8g_rows;
+        e = launch_gemv_i8g(g, cfg, s->stream);
         if (e != hipSuccess) return hip_fail(e, "i8g gemv launch");
     }
     return INGOT_OK;
@@ -547,7 +551,7 @@ static int gemm_core(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const
     // tiles (on MI355X at K = 2048, M = 8 and 16: N = 6144 10.7 vs 12.7 µs, N =
     // 11264 13.1 vs 16.2 µs; N = 2048 the GEMV stays ahead, 8.7 vs 10.4 µs).
     if (w->kind == KIND_BF16 && a->M <= 16 && (a->M <= 4 || a->N < 4096) && !a->trans_a &&
-        a->a_dtype == INGOT_DT_F32 && batch == 1 && !getenv("INGOT_NO_GEMV"))
+        a->a_dtype == INGOT_DT_F32 && batch == 1 && !s->no_gemv)
         return run_gemv(s, a, w);
 
     // bf16 weights with f32 activations: two bf16 planes (f32-class accuracy)
@@ -602,7 +606,7 @@ static int gemm_core(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const
     g.y = a->d_y;
     g.ldy = a->ldy;
     g.epi = make_epi(a);
-    const int cfg = pick_config(kind, a->M, a->N, batch, s->num_cus);
+    const int cfg = pick_config(kind, a->M, a->N, batch, s->num_cus, s->force_gemm_cfg);
     const GemmConfig* c;
     gemm_configs(kind, &c);
     g.tiles_m = (int)((a->M + c[cfg].bm - 1) / c[cfg].bm);
@@ -724,7 +728,7 @@ static int qgemm(ingot_rocm_session* s, int64_t M, int64_t N, int64_t K, const v
     g.qepi.yq_u8 = yq_u8;
     g.qepi.rq_mult = rq_mult;
     g.qepi.rq_zy = rq_zy;
-    const int cfg = pick_config(KIND_I8, M, N, 1, s->num_cus);
+    const int cfg = pick_config(KIND_I8, M, N, 1, s->num_cus, s->force_gemm_cfg);
     const GemmConfig* c;
     gemm_configs(KIND_I8, &c);
     g.tiles_m = (int)((M + c[cfg].bm - 1) / c[cfg].bm);
@@ -797,8 +801,7 @@ int ingot_rocm_qlinear_conv(ingot_rocm_session* s, const ingot_rocm_qconv_args* 
     // Route: a GEMM needs output-channel and reduction width to fill MFMA
     // tiles; depthwise and narrow groups run direct. INGOT_QCONV_PATH=1/2
     // forces direct/GEMM (tests run both routes on the same cases).
-    const char* force = getenv("INGOT_QCONV_PATH");
-    const int path = force && *force ? atoi(force) : 0;
+    const int path = s->qconv_path;
     const int64_t kgl = round_up(K, 128);
     const bool gemm = path == 2 || (path != 1 && Mg >= 16 && K >= 32);
     if (!gemm) {
@@ -818,7 +821,7 @@ int ingot_rocm_qlinear_conv(ingot_rocm_session* s, const ingot_rocm_qconv_args* 
     void* ws;
     rc = ws_reserve(s, (size_t)(a->group * ipc * per_img), &ws);
     if (rc) return rc;
-    const int cfg0 = pick_config(KIND_I8, ipc * P, Mg, a->group, s->num_cus);
+    const int cfg0 = pick_config(KIND_I8, ipc * P, Mg, a->group, s->num_cus, s->force_gemm_cfg);
     const GemmConfig* cf;
     gemm_configs(KIND_I8, &cf);
     for (int64_t n0 = 0; n0 < a->n; n0 += ipc) {
@@ -855,7 +858,7 @@ int ingot_rocm_qlinear_conv(ingot_rocm_session* s, const ingot_rocm_qconv_args* 
         ga.qepi.col_batch = (int32_t)Mg;
         ga.qepi.conv_p = (int32_t)P;
         ga.qepi.conv_img = a->m * P;
-        const int cfg = rows == ipc * P ? cfg0 : pick_config(KIND_I8, rows, Mg, a->group, s->num_cus);
+        const int cfg = rows == ipc * P ? cfg0 : pick_config(KIND_I8, rows, Mg, a->group, s->num_cus, s->force_gemm_cfg);
         ga.tiles_m = (int)((rows + cf[cfg].bm - 1) / cf[cfg].bm);
         ga.tiles_n = (int)((Mg + cf[cfg].bn - 1) / cf[cfg].bn);
         e = launch_gemm(KIND_I8, cfg, ga, (int)a->group, s->stream);

@@ -26,6 +26,17 @@ struct ingot_rocm_session {
     hipEvent_t t0 = nullptr, t1 = nullptr;
     void* ws = nullptr;  // workspace: packed activations (bf16 A planes, GEMV x planes, int8 A, im2col)
     size_t ws_bytes = 0;
+    // Test and bisection hooks, read once when the session opens (a launch
+    // must not pay for getenv): INGOT_GEMM_CFG forces a GEMM tile
+    // configuration, INGOT_GEMV_CFG a GEMV launch configuration,
+    // INGOT_I8G_ROWS the int8 GEMV rows per wave, INGOT_NO_GEMV sends decode
+    // rows to the GEMM, INGOT_QCONV_PATH forces QLinearConv's route (1 direct,
+    // 2 GEMM). -1 / 0 / false: not set.
+    int force_gemm_cfg = -1;
+    int force_gemv_cfg = 0;
+    int i8g_rows = 0;
+    bool no_gemv = false;
+    int qconv_path = 0;
     std::vector<ingot_rocm_weight*> weights;
     std::map<size_t, std::vector<void*>> free_bufs;    // pool: size class → free buffers
     std::unordered_map<void*, size_t> buf_class;       // pool: buffer → size class

@@ -100,6 +100,12 @@ class Op:
             res.append(DeviceTensor(self.sess, o.dtype, [o.dims[d] for d in range(o.rank)], o.data, False, True))
         return res
 
+    def set_const(self, *inputs: int) -> "Op":
+        """Declares inputs constant (same storage and values every run): the op may pack them once."""
+        for i in inputs:
+            L.check(self.sess.lib.ingot_rocm_op_set_const(self.h, i, 1))
+        return self
+
     def free(self) -> None:
         if self.h:
             L.check(self.sess.lib.ingot_rocm_op_free(self.h))

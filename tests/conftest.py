@@ -21,3 +21,23 @@ def sess():
     s = Session(0)
     yield s
     s.close()
+
+
+@pytest.fixture
+def env_session(monkeypatch):
+    """Opens extra library sessions with INGOT_* test hooks set (INGOT_GEMM_CFG, INGOT_GEMV_CFG, INGOT_I8G_ROWS,
+    INGOT_NO_GEMV, INGOT_QCONV_PATH): a session reads them once, when it opens."""
+    from ingot_amd import Session
+
+    opened = []
+
+    def open_with(**env):
+        for k, v in env.items():
+            monkeypatch.setenv(k, str(v))
+        s = Session(0)
+        opened.append(s)
+        return s
+
+    yield open_with
+    for s in opened:
+        s.close()

@@ -224,10 +224,10 @@ def test_gemv_i8g_exact(sess, m, src, n, k):
 
 @pytest.mark.parametrize("rows", ["1", "2", "4"])
 @pytest.mark.parametrize("m", [1, 2, 4])
-def test_gemv_i8g_rows_per_wave(sess, monkeypatch, rows, m):
+def test_gemv_i8g_rows_per_wave(env_session, rows, m):
     """Every rows-per-wave variant of the int8 GEMV (INGOT_I8G_ROWS), ragged N, bit-exact."""
     announce(f"i8g rows={rows} m={m}")
-    monkeypatch.setenv("INGOT_I8G_ROWS", rows)
+    sess = env_session(INGOT_I8G_ROWS=rows)
     rng = np.random.default_rng(int(rows) * 10 + m)
     n, k = 301, 1216
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
@@ -304,9 +304,9 @@ GEMM_CFGS = {"f32": range(5), "bf16": range(9), "bf16x2": range(5), "i8": range(
 
 @pytest.mark.parametrize("kind,cfg", [(k, c) for k, r in GEMM_CFGS.items() for c in r])
 @pytest.mark.parametrize("m,n,k", [(70, 197, 300), (257, 100, 1030)])
-def test_gemm_forced_tile_configs(sess, monkeypatch, kind, cfg, m, n, k):
+def test_gemm_forced_tile_configs(env_session, kind, cfg, m, n, k):
     announce(f"gemm forced tile kind={kind} cfg={cfg} m={m} n={n} k={k}")
-    monkeypatch.setenv("INGOT_GEMM_CFG", str(cfg))
+    sess = env_session(INGOT_GEMM_CFG=cfg)
     rng = np.random.default_rng(cfg * 1009 + m * 7 + n + k)
     if kind == "i8":
         a = rng.integers(0, 256, (m, k)).astype(np.uint8)
@@ -343,7 +343,7 @@ def test_gemm_forced_tile_configs(sess, monkeypatch, kind, cfg, m, n, k):
 @pytest.mark.parametrize("cfg", ["10", "11", "12", "13", "14", "15", "16", "17", "18", "19", "20", "21", "22",
                                  "1", "2", "3", "4", "5", "6", "7"])
 @pytest.mark.parametrize("m", [1, 2, 4, 9, 16])
-def test_gemv_forced_configs(sess, monkeypatch, cfg, m):
+def test_gemv_forced_configs(env_session, cfg, m):
     """Every GEMV launch configuration (INGOT_GEMV_CFG) that applies to M, strided x, both math modes."""
     rows_cfg = int(cfg) >= 10
     mm = {"10": 1, "11": 1, "12": 1, "13": 4, "14": 4, "15": 2, "16": 4, "17": 4, "18": 4, "19": 2,
@@ -351,7 +351,7 @@ def test_gemv_forced_configs(sess, monkeypatch, cfg, m):
     if (m > 4) == rows_cfg or m > mm:
         pytest.skip("configuration does not cover this M")
     announce(f"gemv cfg={cfg} m={m}")
-    monkeypatch.setenv("INGOT_GEMV_CFG", cfg)
+    sess = env_session(INGOT_GEMV_CFG=cfg)
     rng = np.random.default_rng(int(cfg) * 31 + m)
     n, k, lda = 328, 1300, 1309
     xs = rng.normal(0, 1, (m, lda)).astype(np.float32)
@@ -463,7 +463,9 @@ def test_config5_dit_bf16(sess, k, n, act):
     w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
     da = sess.to_device(a)
     got = run_gemm(sess, da, w, 4096, act=act, math=L.MATH_BF16)
-    rows = np.arange(5, 4096, 257)
+    # 256 rows covering every residue mod 256: every wave row and every 16-row MFMA block of every tile
+    rows = (np.arange(256) * 17 + 5) % 4096
+    assert len(set(rows % 256)) == 256
     want = oracle.gemm(a[rows], wb, trans_b=True, b_dtype=oracle.BF16, act_code=act)
     assert_close(got[rows], want, nstar_tol(k, a, oracle.bf16_to_f32(wb)), f"dit {k}x{n}")
     assert np.array_equal(run_gemm(sess, da, w, 4096, act=act, math=L.MATH_BF16), got), "run-to-run bit identity"
@@ -476,7 +478,8 @@ def test_config5_dit_bf16(sess, k, n, act):
 @pytest.mark.parametrize("m", [1, 4, 16])
 @pytest.mark.parametrize("k,n", [(2048, 6144), (2048, 2048), (2048, 11264), (5632, 2048)])
 def test_config4_decode_gemv(sess, m, k, n):
-    """Llama-style decode, bf16 weights, M in {1,4,16} (Gemm op path: M <= 16 → GEMV)."""
+    """Llama-style decode, bf16 weights, M in {1,4,16} (M <= 4, and M = 16 with N < 4096, run the
+    GEMV; M = 16 with N >= 4096 the hi/lo GEMM)."""
     announce(f"decode m={m} k={k} n={n}")
     rng = np.random.default_rng(m + k + n)
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
@@ -486,3 +489,151 @@ def test_config4_decode_gemv(sess, m, k, n):
     want = oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16)
     assert_close(got, want, nstar_tol(k, x, oracle.bf16_to_f32(wb)), f"decode {m}x{k}x{n}")
     w.free()
+
+
+@pytest.mark.parametrize("m", [5, 9, 16])
+@pytest.mark.parametrize("n", [4095, 4096, 6144])
+def test_decode_rows_gemm_route(sess, m, n):
+    """M = 5..16 rows of f32 A against bf16 weights: N < 4096 runs the GEMV, N >= 4096 the hi/lo GEMM of
+    four-stage 32x32 tiles. Both sides of the boundary with a per-column bias, GELU, and f32 and bf16 Y; f32 Y
+    is held to the reference's bf16-weight bound (relative 1e-5·sqrt(K), ops/gemm_bf16_optest_test.go:57)
+    against the float64 oracle, bf16 Y additionally to one bf16 rounding of the result."""
+    announce(f"decode rows route m={m} n={n}")
+    k = 2048
+    rng = np.random.default_rng(m * 10007 + n)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    dx, db = sess.to_device(x), sess.to_device(bias)
+    want = oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16, beta=1.0, c=bias, c_mode=L.C_ROW,
+                       act_code=L.ACT_GELU_ERF)
+    y = sess.empty(L.DT_F32, (m, n))
+    sess.gemm(dx, w, y, m, beta=1.0, c=db, c_mode=L.C_ROW, act=L.ACT_GELU_ERF)
+    got = y.numpy()
+    rel = np.max(np.abs(got - want) / (1 + np.abs(want)))
+    assert rel <= 1e-5 * math.sqrt(k), f"f32 Y relative error {rel:.3e}"
+    yb = sess.empty(L.DT_BF16, (m, n))
+    sess.gemm(dx, w, yb, m, beta=1.0, c=db, c_mode=L.C_ROW, act=L.ACT_GELU_ERF)
+    gotb = oracle.bf16_to_f32(yb.numpy())
+    relb = np.max(np.abs(gotb - want) / (1 + np.abs(want)))
+    assert relb <= 2.0 ** -8 + 1e-5 * math.sqrt(k), f"bf16 Y relative error {relb:.3e}"
+    # the bf16 store is the RNE rounding of the f32 result of the same route
+    assert np.array_equal(yb.numpy(), oracle.f32_to_bf16(got))
+    w.free()
+
+
+SENTINEL = np.float32(1e9)
+
+
+def dirty_rows(sess, m, n, ldy, dtype=L.DT_F32):
+    """A destination of m rows of pitch ldy (>= n), every element set to SENTINEL (bf16: its bf16 bits)."""
+    host = np.full((m, ldy), SENTINEL, np.float32)
+    if dtype == L.DT_BF16:
+        host = oracle.f32_to_bf16(host)
+    return sess.to_device(host, dtype), host
+
+
+def check_padded(got_full, want, n, tol, what, sentinel_bits=None):
+    """The first n columns match the oracle; columns n..ldy keep the sentinel."""
+    assert_close(got_full[:, :n], want, tol, what)
+    pad = got_full[:, n:]
+    if sentinel_bits is None:
+        assert np.all(pad == SENTINEL), f"{what}: row padding written"
+    else:
+        assert np.all(pad == sentinel_bits), f"{what}: row padding written"
+
+
+@pytest.mark.parametrize("pad", [3, 4])
+@pytest.mark.parametrize("route", ["f32", "bf16", "bf16x2", "gemv_m3", "gemv_m9", "gemm_m9", "bf16_y"])
+def test_dirty_padded_destination(sess, route, pad):
+    """The destination starts dirty (1e9 everywhere, as kernels/metal/gemmep_test.go:45-47) with row pitch
+    ldy = N + pad: every output is overwritten and the padding past N stays untouched
+    (kernels/metal/gemmep_test.go:22-96, kernels/metal/gemm_test.go:14,45). pad = 3 makes the pitch unaligned
+    (scalar stores), pad = 4 keeps 16-byte rows (vector stores)."""
+    announce(f"dirty padded destination route={route} pad={pad}")
+    rng = np.random.default_rng(len(route) * 101 + pad)
+    m, n, k = {"gemv_m3": (3, 300, 640), "gemv_m9": (9, 300, 640), "gemm_m9": (9, 4100, 512)}.get(route, (70, 197, 300))
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    kw = dict(beta=1.0, c=sess.to_device(bias), c_mode=L.C_ROW, act=L.ACT_GELU_ERF)
+    ldy = n + pad
+    if route == "f32":
+        bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+        w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_F32)
+        wide, okw = bt, {}
+    else:
+        bt = bf16_weights(rng, (n, k))
+        w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+        wide, okw = oracle.bf16_to_f32(bt), {"b_dtype": oracle.BF16}
+        if route == "bf16":
+            kw["math"] = L.MATH_BF16
+    ain = oracle.bf16_to_f32(oracle.f32_to_bf16(a)) if route == "bf16" else a
+    want = oracle.gemm(np.ascontiguousarray(ain), bt, trans_b=True, c=bias, c_mode=L.C_ROW, beta=1.0,
+                       act_code=L.ACT_GELU_ERF, **okw)
+    tol = nstar_tol(k, a, wide)
+    if route == "bf16_y":
+        y, host = dirty_rows(sess, m, n, ldy, L.DT_BF16)
+        sess.gemm(sess.to_device(a), w, y, m, ldy=ldy, **kw)
+        got = y.numpy()
+        assert np.array_equal(got[:, n:], host[:, n:]), "bf16 Y: row padding written"
+        assert_close(oracle.bf16_to_f32(got[:, :n]), want, tol + 2.0 ** -8 * np.abs(want).max(), "bf16 Y")
+    else:
+        y, _ = dirty_rows(sess, m, n, ldy)
+        sess.gemm(sess.to_device(a), w, y, m, ldy=ldy, **kw)
+        check_padded(y.numpy(), want, n, tol, route)
+    w.free()
+
+
+def test_dirty_destination_int8(sess):
+    """MatMulInteger + fused dequant into dirty outputs (1e9 / 0x7f7f7f7f) followed by guard elements: every
+    output overwritten (bit-exact), the guard elements past M·N untouched."""
+    announce("dirty destination int8")
+    rng = np.random.default_rng(99)
+    m, n, k = 70, 197, 300
+    a = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    sc = rng.uniform(0.001, 0.01, n).astype(np.float32)
+    w = sess.upload_weight(b, trans=False, pack_dtype=L.DT_I8)
+    guard = 37
+    yi = sess.to_device(np.full(m * n + guard, 0x7F7F7F7F, np.int32))
+    yf = sess.to_device(np.full(m * n + guard, SENTINEL, np.float32))
+    sess.matmul_integer(sess.to_device(a, L.DT_U8), w, m, 128, y_i32=yi, scale=sess.to_device(sc), y_f32=yf)
+    want = oracle.matmul_integer(a, b, 128)
+    gi, gf = yi.numpy(), yf.numpy()
+    assert np.array_equal(gi[:m * n].reshape(m, n), want)
+    assert np.array_equal(gf[:m * n].reshape(m, n), oracle.dequantize_linear(want, sc, inner=1))
+    assert np.all(gi[m * n:] == 0x7F7F7F7F) and np.all(gf[m * n:] == SENTINEL)
+    w.free()
+
+
+def test_m_invariance(sess):
+    """Rows are bit-identical whatever M is (kernels/gemm/minvariance_test.go:21), where the same kernel kind runs:
+    every GEMM tile configuration of one kind reduces K in the same order (k-tile after k-tile, the same MFMA per
+    16-byte k chunk), so the tile choice, which follows M, does not change a row. f32 weights: every M (f32
+    weights never take the GEMV). bf16 weights with f32 A: every M >= 17, and M = 5..16 when N >= 4096 (the same
+    hi/lo GEMM); the decode GEMV (M <= 4, and M = 5..16 with N < 4096) sums in another order, like the
+    reference's exempt M = 1 GEMV. int8 is exact, hence invariant."""
+    announce("m invariance")
+    rng = np.random.default_rng(2024)
+    k = 1100
+    a = rng.normal(0, 1, (600, k)).astype(np.float32)
+    da = sess.to_device(a)
+
+    def rows_of(w, n, M, **kw):
+        y = sess.empty(L.DT_F32, (M, n))
+        sess.gemm(da, w, y, M, **kw)
+        return y.numpy()
+
+    n = 4200
+    wf = sess.upload_weight(rng.normal(0, 0.05, (n, k)).astype(np.float32), trans=True, pack_dtype=L.DT_F32)
+    full = rows_of(wf, n, 600)
+    for M in (1, 3, 16, 33, 129, 257):
+        assert np.array_equal(rows_of(wf, n, M), full[:M]), f"f32 weights M={M}"
+    wb = sess.upload_weight(bf16_weights(rng, (n, k), 0.05, "normal"), trans=True, pack_dtype=L.DT_BF16,
+                            src_dtype=L.DT_BF16)
+    for kw in ({}, {"math": L.MATH_BF16}):
+        full = rows_of(wb, n, 600, **kw)
+        for M in (5, 9, 16, 17, 40, 129, 300):
+            assert np.array_equal(rows_of(wb, n, M, **kw), full[:M]), f"bf16 weights M={M} {kw}"
+    wf.free(), wb.free(), da.free()

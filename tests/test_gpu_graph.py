@@ -101,3 +101,38 @@ def test_graph_unfused_add_is_declined(sess):
             g2.bind(k, v)
         g2.compile(L.GRAPH_FUSE_BIAS)
         g2.run({})
+
+
+DYN_RHS = """
+input x f32 {m},{k}
+input z f32 {k},{n}
+node Relu z -> rz
+node MatMul x,rz -> y
+output y
+"""
+
+
+def test_graph_dynamic_rhs_packed_per_run(sess):
+    """MatMul(x, Relu(z)) with a 2-D z that is a graph input, not a constant: the right operand is a pooled
+    intermediate that comes back at the same device address with new contents on the next run, so it must be
+    packed per run (the reference's GPU session caches only graph constants: graph/gpuops_darwin_arm64.go:610-629).
+    Two runs with different z, each against the float64 product (f32 tolerance 1e-5·sqrt(K) relative,
+    kernels/gemm/gemm_test.go:34)."""
+    announce("graph dynamic rhs")
+    m, k, n = 96, 320, 200
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    g = Graph(sess, DYN_RHS.format(m=m, k=k, n=n))
+    g.compile(L.GRAPH_FUSE_BIAS | L.GRAPH_FUSE_ACT)
+    dx = sess.to_device(x)
+    for run in range(2):
+        z = rng.normal(0, 1, (k, n)).astype(np.float32)
+        dz = sess.to_device(z)
+        (y,) = g.run({"x": dx, "z": dz})
+        want = x.astype(np.float64) @ np.maximum(z, 0).astype(np.float64)
+        got = y.numpy()
+        y.free()
+        dz.free()
+        err = np.max(np.abs(got - want)) / max(1.0, np.max(np.abs(want)))
+        assert err <= 1e-5 * math.sqrt(k), f"run {run}: relative error {err:.3e}"
+    g.free()

@@ -289,3 +289,60 @@ def test_activation_nodes(sess, name, domain, attrs, code):
                dev(sess, x))
     want = np.vectorize(lambda v: oracle.act(v, code))(x.astype(np.float64))
     assert_close(y, want, 2e-6 * max(1.0, float(np.max(np.abs(want)))), name)
+
+
+def test_refilled_weight_buffer_is_repacked(sess):
+    """An operand not declared constant is packed per call: the same device buffer refilled with new values
+    between runs gives the new product (Gemm f32 and bf16 B, MatMul, MatMulInteger). A declared-constant B
+    (ingot_rocm_op_set_const) is packed once and reused on later runs."""
+    announce("op refilled weight buffer")
+    rng = np.random.default_rng(17)
+    m, k, n = 40, 192, 136
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    da = dev(sess, a)
+    cases = [("Gemm", 13, {"transB": 1}, lambda b: b.T), ("MatMul", 13, {}, lambda b: b)]
+    for name, opset, attrs, orient in cases:
+        op = sess.op(name, opset, attrs)
+        shape = (n, k) if attrs.get("transB") else (k, n)
+        db = sess.empty(L.DT_F32, shape)
+        for rep in range(2):
+            b = rng.normal(0, 1, shape).astype(np.float32)
+            L.check(sess.lib.ingot_rocm_memcpy_h2d(sess.h, db.ptr, b.ctypes.data, b.nbytes))
+            (y,) = run(op, da, db)
+            want = a.astype(np.float64) @ orient(b).astype(np.float64)
+            err = np.max(np.abs(y - want)) / max(1.0, np.max(np.abs(want)))
+            assert err <= 1e-5 * np.sqrt(k), f"{name} run {rep}: relative error {err:.3e}"
+        op.free()
+    # bf16 B bits refilled in place (Gemm, transB)
+    op = sess.op("Gemm", 13, {"transB": 1})
+    db = sess.empty(L.DT_BF16, (n, k))
+    for rep in range(2):
+        wb = bf16_weights(rng, (n, k), 0.5)
+        L.check(sess.lib.ingot_rocm_memcpy_h2d(sess.h, db.ptr, wb.ctypes.data, wb.nbytes))
+        (y,) = run(op, da, db)
+        want = oracle.gemm(a, wb, trans_b=True, b_dtype=oracle.BF16)
+        assert_close(y, want, nstar_tol(k, a, oracle.bf16_to_f32(wb)), f"gemm bf16 B run {rep}")
+    op.free()
+    # MatMulInteger: int8 B refilled in place
+    qa = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    op = sess.op("MatMulInteger", 10)
+    dqa = dev(sess, qa, L.DT_U8)
+    dqb = sess.empty(L.DT_I8, (k, n))
+    for rep in range(2):
+        qb = rng.integers(-127, 128, (k, n)).astype(np.int8)
+        L.check(sess.lib.ingot_rocm_memcpy_h2d(sess.h, dqb.ptr, qb.ctypes.data, qb.nbytes))
+        (y,) = run(op, dqa, dqb, dev(sess, np.array([128], np.uint8), L.DT_U8))
+        assert np.array_equal(y, oracle.matmul_integer(qa, qb, 128)), f"matmul_integer run {rep}"
+    op.free()
+    # a declared constant is packed once: refilling its storage afterwards is outside the contract, and the
+    # cached pack (the first values) is what later runs multiply by
+    op = sess.op("MatMul", 13).set_const(1)
+    db = sess.empty(L.DT_F32, (k, n))
+    b0 = rng.normal(0, 1, (k, n)).astype(np.float32)
+    L.check(sess.lib.ingot_rocm_memcpy_h2d(sess.h, db.ptr, b0.ctypes.data, b0.nbytes))
+    (y0,) = run(op, da, db)
+    b1 = rng.normal(0, 1, (k, n)).astype(np.float32)
+    L.check(sess.lib.ingot_rocm_memcpy_h2d(sess.h, db.ptr, b1.ctypes.data, b1.nbytes))
+    (y1,) = run(op, da, db)
+    assert np.array_equal(y0, y1)
+    op.free()

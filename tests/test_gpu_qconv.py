@@ -7,7 +7,6 @@ shapes that take the im2col → int8 MFMA GEMM route. Both device routes
 (direct, GEMM) run every case: INGOT_QCONV_PATH=1 forces the direct kernel,
 2 the GEMM.
 """
-import os
 
 import numpy as np
 import pytest
@@ -23,15 +22,18 @@ pytestmark = pytest.mark.gpu
 DT = {np.dtype(np.uint8): L.DT_U8, np.dtype(np.int8): L.DT_I8}
 
 
-@pytest.fixture(params=["auto", "direct", "gemm"])
+ROUTES = {"auto": "0", "direct": "1", "gemm": "2"}
+
+
+@pytest.fixture(params=list(ROUTES))
 def route(request):
-    old = os.environ.get("INGOT_QCONV_PATH")
-    os.environ["INGOT_QCONV_PATH"] = {"auto": "0", "direct": "1", "gemm": "2"}[request.param]
-    yield request.param
-    if old is None:
-        del os.environ["INGOT_QCONV_PATH"]
-    else:
-        os.environ["INGOT_QCONV_PATH"] = old
+    return request.param
+
+
+@pytest.fixture
+def qsess(env_session, route):
+    """A session whose QLinearConv route is forced (INGOT_QCONV_PATH, read when the session opens)."""
+    return env_session(INGOT_QCONV_PATH=ROUTES[route])
 
 
 def make_case(rng, n, c, h, w, m, kh, kw, g, x_dtype=np.uint8, zx=120, with_bias=True, per_channel=True):
@@ -72,7 +74,8 @@ def run_conv(sess, x, zx, wt, bias, mult, zy, y_u8, group=1, strides=(1, 1), dil
 
 @pytest.mark.parametrize("cfg", REF_CFGS, ids=[f"c{i}" for i in range(len(REF_CFGS))])
 @pytest.mark.parametrize("x_dtype,zx,y_u8,zy", [(np.uint8, 120, True, 17), (np.int8, -7, False, -3)])
-def test_reference_geometries(sess, route, cfg, x_dtype, zx, y_u8, zy):
+def test_reference_geometries(qsess, route, cfg, x_dtype, zx, y_u8, zy):
+    sess = qsess
     n, c, h, w, m, kh, kw, g, sh, sw, pt, pl = cfg
     announce(f"qconv ref cfg {cfg} x={np.dtype(x_dtype).name} route={route}")
     rng = np.random.default_rng(hash(cfg) % 2**32)
@@ -98,7 +101,8 @@ GEMM_CASES = [
 
 
 @pytest.mark.parametrize("case", GEMM_CASES, ids=[f"g{i}" for i in range(len(GEMM_CASES))])
-def test_gemm_shapes(sess, route, case):
+def test_gemm_shapes(qsess, route, case):
+    sess = qsess
     n, c, h, w, m, kh, kw, g, st, dl, pads = case
     if route == "direct" and c * h * w * m * kh * kw // g > 5e7:
         pytest.skip("the direct route is covered on the smaller cases")
@@ -114,24 +118,15 @@ def test_gemm_shapes(sess, route, case):
         assert len(np.unique(got)) > 16  # not saturated wholesale
 
 
-def test_routes_agree_at_size(sess):
+def test_routes_agree_at_size(env_session):
     """A ResNet-stage conv (1×256×56×56 → 256, 3×3, pad 1): GEMM and direct routes are both exact, so they
     agree bit for bit; a slab of output channels is checked against the oracle."""
     announce("qconv routes at size")
     rng = np.random.default_rng(56)
     x, zx, wt, bias, mult, *_ = make_case(rng, 1, 256, 56, 56, 256, 3, 3, 1)
     pads = (1, 1, 1, 1)
-    old = os.environ.get("INGOT_QCONV_PATH")
-    try:
-        os.environ["INGOT_QCONV_PATH"] = "2"
-        y_gemm = run_conv(sess, x, zx, wt, bias, mult, 17, True, pads=pads)
-        os.environ["INGOT_QCONV_PATH"] = "1"
-        y_dir = run_conv(sess, x, zx, wt, bias, mult, 17, True, pads=pads)
-    finally:
-        if old is None:
-            os.environ.pop("INGOT_QCONV_PATH", None)
-        else:
-            os.environ["INGOT_QCONV_PATH"] = old
+    y_gemm = run_conv(env_session(INGOT_QCONV_PATH=2), x, zx, wt, bias, mult, 17, True, pads=pads)
+    y_dir = run_conv(env_session(INGOT_QCONV_PATH=1), x, zx, wt, bias, mult, 17, True, pads=pads)
     np.testing.assert_array_equal(y_gemm, y_dir)
     sl = slice(100, 108)
     want = oracle.qlinear_conv(x, zx, wt[sl], bias[sl], mult[sl], 17, True, pads=pads)
