@@ -216,6 +216,21 @@ typedef struct ingot_rocm_gemm_args {
 
 int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* args);
 
+/* ingot_rocm_gemm without any allocation: the same validation, routing and
+ * kernels, with the per-call scratch (packed activations, the decode GEMV's x
+ * planes, the int8 GEMV's quantised x) in a fixed device array of
+ * INGOT_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, instead
+ * of the session's growable workspace. No hipMalloc, hipFree or allocating
+ * library routine runs in the call. A product needing more scratch fails with
+ * INGOT_EINVAL and a message naming the size. No counterpart in the
+ * reference: it is for callers that cannot allocate (HIP graph capture, tight
+ * serving loops, harnesses that forbid it). The array is shared by every call
+ * on that GPU, from any session or stream, and keeps the last call's contents
+ * (each call writes every scratch byte it reads): calls that overlap on one GPU
+ * race, so the caller serialises them. */
+#define INGOT_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int ingot_rocm_gemm_noalloc(ingot_rocm_session* s, const ingot_rocm_gemm_args* args);
+
 /* Batched GEMM whose B is an activation: each batch item i multiplies its A
  * (stride_a) by its own B at d_b + i·stride_b elements (stride_b 0: one B for
  * every item), packed on the device per call. B items are [N,K] with row

@@ -12,6 +12,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libingot_rocm.so")
 
+NOALLOC_SCRATCH_BYTES = 32 << 20  # INGOT_NOALLOC_SCRATCH_BYTES
 # status codes
 OK, EINVAL, EDECLINED, EDEVICE, ENOMEM = 0, 1, 2, 3, 4
 # dtypes (tensor/dtype.go:12-23)
@@ -90,6 +91,7 @@ SIGNATURES = {
     "ingot_rocm_graph_describe": (C.c_int, [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t]),
     "ingot_rocm_graph_free": (C.c_int, [C.c_void_p]),
     "ingot_rocm_gemm": (C.c_int, [C.c_void_p, C.POINTER(GemmArgs)]),
+    "ingot_rocm_gemm_noalloc": (C.c_int, [C.c_void_p, C.POINTER(GemmArgs)]),
     "ingot_rocm_gemm_dynamic_b": (C.c_int, [C.c_void_p, C.POINTER(GemmArgs), C.c_void_p, C.c_int32, C.c_int32,
                                             C.c_int64, C.c_int64]),
     "ingot_rocm_gemv_bf16": (C.c_int, [C.c_void_p, C.POINTER(GemmArgs)]),

@@ -15,8 +15,22 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 using namespace ingot;
+
+// Fixed device scratch of ingot_rocm_gemm_noalloc: the packed activations
+// (bf16 / hi-lo planes, the decode GEMV's x planes, the int8 GEMV's
+// quantised x) that ingot_rocm_gemm keeps in the session's growable
+// workspace. Each device holds its own copy for the life of the process. In
+// host code `scratch` only names the symbol: its device address comes from
+// hipGetSymbolAddress, once per device (g_scratch_addr), and only that
+// address is handed to kernels.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[kMaxDevices];
 
 namespace {
 
@@ -111,6 +125,17 @@ int ws_reserve(ingot_rocm_session* s, size_t bytes, void** out) {
     return INGOT_OK;
 }
 
+// The workspace of one call: the session's growable buffer, or with noalloc
+// the device's fixed scratch array (no allocation; sizes beyond it fail).
+int call_ws(ingot_rocm_session* s, bool noalloc, size_t bytes, void** out) {
+    if (!noalloc) return ws_reserve(s, bytes, out);
+    if (bytes > kNoAllocScratchBytes)
+        return fail(INGOT_EINVAL, "gemm_noalloc: the call needs %zu bytes of scratch; the fixed maximum is %zu", bytes,
+                    kNoAllocScratchBytes);
+    *out = s->scratch;
+    return INGOT_OK;
+}
+
 void* pool_get(ingot_rocm_session* s, size_t bytes) {
     size_t cls = 256;
     while (cls < bytes) cls <<= 1;
@@ -185,9 +210,22 @@ int ingot_rocm_open(int device, ingot_rocm_session** out) {
     if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(INGOT_EDEVICE, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+    if (device >= kMaxDevices) return fail(INGOT_EINVAL, "device %d: at most %d devices", device, kMaxDevices);
+    {
+        // with `device` current: its copy of the no-alloc scratch array
+        std::lock_guard<std::mutex> g(g_scratch_mu);
+        if (!g_scratch_addr[device]) {
+            void* p = nullptr;
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+            if (!p) return fail(INGOT_EDEVICE, "hipGetSymbolAddress(scratch) returned no address");
+            g_scratch_addr[device] = p;
+        }
+    }
     auto* s = new ingot_rocm_session();
     s->device = device;
     s->num_cus = prop.multiProcessorCount;
+    s->scratch = g_scratch_addr[device];
     auto env_int = [](const char* name, int dflt) {
         const char* v = getenv(name);
         return v && *v ? atoi(v) : dflt;
@@ -429,7 +467,8 @@ int ingot_rocm_weight_info(const ingot_rocm_weight* w, int64_t* n, int64_t* k, i
 
 // ---------------- GEMM / GEMV ----------------
 
-static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w) {
+static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w,
+                    bool noalloc = false) {
     GemvArgs g;
     memset(&g, 0, sizeof g);
     g.x = (const float*)a->d_a;
@@ -448,7 +487,7 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const 
     if (a->M > 4) {
         // the MFMA kernel reads x as fragment-ordered bf16 planes (hi, lo)
         void* ws;
-        int rc = ws_reserve(s, (size_t)((g.split ? 2 : 1) * 16 * w->kp * 2), &ws);
+        int rc = call_ws(s, noalloc, (size_t)((g.split ? 2 : 1) * 16 * w->kp * 2), &ws);
         if (rc) return rc;
         hipError_t e = launch_pack_x((const float*)a->d_a, a->lda, (int)a->M, (int)a->K, w->kp, g.split,
                                      (uint16_t*)ws, s->stream);
@@ -464,13 +503,14 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const 
 
 // Grouped-int8 GEMV: x split once per call into the workspace, then one
 // launch per 4 activation rows.
-static int run_gemv_i8g(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w) {
+static int run_gemv_i8g(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w,
+                        bool noalloc) {
     const int64_t kp = w->kp, gk = kp / 64;
     if (gk * 4 * 4 * (int64_t)sizeof(float) > 64 * 1024)
         return fail(INGOT_EDECLINED, "gemm: I8G GEMV supports K up to 65536");
     void* ws;
     const size_t plane = (size_t)(a->M * kp);
-    int rc = ws_reserve(s, 2 * plane + (size_t)(a->M * gk) * sizeof(float) + 256, &ws);
+    int rc = call_ws(s, noalloc, 2 * plane + (size_t)(a->M * gk) * sizeof(float) + 256, &ws);
     if (rc) return rc;
     int8_t* xh = (int8_t*)ws;
     int8_t* xl = xh + plane;
@@ -538,21 +578,22 @@ int ingot_rocm_gemv_bf16(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
 
 // The GEMM after validation. w may be a session weight or a per-call packed
 // operand; stride_b_bytes advances it per batch item (0: shared).
-static int run_gemv_i8g(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w);
+static int run_gemv_i8g(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w,
+                        bool noalloc);
 
 static int gemm_core(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const ingot_rocm_weight* w,
-                     int64_t stride_b_bytes) {
+                     int64_t stride_b_bytes, bool noalloc = false) {
     int rc;
     const int64_t batch = std::max<int64_t>(1, a->batch);
     if (a->M == 0 || a->N == 0) return INGOT_OK;
-    if (w->kind == KIND_I8G) return run_gemv_i8g(s, a, w);
+    if (w->kind == KIND_I8G) return run_gemv_i8g(s, a, w, noalloc);
     // Decode rows take the GEMV: all of M <= 4, and M = 5..16 for N < 4096. At
     // M = 5..16 the wider products run faster as a GEMM of four-stage 32×32
     // tiles (on MI355X at K = 2048, M = 8 and 16: N = 6144 10.7 vs 12.7 µs, N =
     // 11264 13.1 vs 16.2 µs; N = 2048 the GEMV stays ahead, 8.7 vs 10.4 µs).
     if (w->kind == KIND_BF16 && a->M <= 16 && (a->M <= 4 || a->N < 4096) && !a->trans_a &&
         a->a_dtype == INGOT_DT_F32 && batch == 1 && !s->no_gemv)
-        return run_gemv(s, a, w);
+        return run_gemv(s, a, w, noalloc);
 
     // bf16 weights with f32 activations: two bf16 planes (f32-class accuracy)
     // unless the caller asked for single bf16 rounding (INGOT_MATH_BF16).
@@ -585,7 +626,7 @@ static int gemm_core(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const
     } else {
         void* ws;
         const int64_t plane = a->M * kl;
-        rc = ws_reserve(s, (size_t)(batch * planes * plane * esz), &ws);
+        rc = call_ws(s, noalloc, (size_t)(batch * planes * plane * esz), &ws);
         if (rc) return rc;
         hipError_t e = launch_pack_a(a->d_a, a->a_dtype, a->lda, a->trans_a, a->M, a->K, a->stride_a, ws, kind, kl,
                                      planes * plane, (int)batch, s->stream);
@@ -620,6 +661,12 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     int rc = validate_gemm(s, a, a ? a->w : nullptr);
     if (rc) return rc;
     return gemm_core(s, a, a->w, 0);
+}
+
+int ingot_rocm_gemm_noalloc(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
+    int rc = validate_gemm(s, a, a ? a->w : nullptr);
+    if (rc) return rc;
+    return gemm_core(s, a, a->w, 0, true);
 }
 
 int ingot_rocm_gemm_dynamic_b(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const void* d_b, int32_t b_dtype,

@@ -24,6 +24,7 @@ struct ingot_rocm_session {
     int num_cus = 256;
     hipStream_t stream = nullptr;
     hipEvent_t t0 = nullptr, t1 = nullptr;
+    void* scratch = nullptr;  // this device's fixed scratch array (ingot_rocm_gemm_noalloc)
     void* ws = nullptr;  // workspace: packed activations (bf16 A planes, GEMV x planes, int8 A, im2col)
     size_t ws_bytes = 0;
     // Test and bisection hooks, read once when the session opens (a launch

@@ -214,6 +214,11 @@ class Session:
         g = self.gemm_args(a, w, y, M, **kw)
         L.check(self.lib.ingot_rocm_gemm(self.h, C.byref(g)))
 
+    def gemm_noalloc(self, a: DeviceTensor, w: Weight, y: DeviceTensor, M: int, **kw) -> None:
+        """ingot_rocm_gemm_noalloc: the same product with its scratch in the fixed per-GPU array."""
+        g = self.gemm_args(a, w, y, M, **kw)
+        L.check(self.lib.ingot_rocm_gemm_noalloc(self.h, C.byref(g)))
+
     def prepare_gemm(self, a: DeviceTensor, w: Weight, y: DeviceTensor, M: int, **kw):
         """ingot_rocm_gemm with its argument block built once: a callable that
         enqueues the same product again (what a compiled session does per node)."""
