@@ -637,3 +637,4 @@ def test_m_invariance(sess):
         for M in (5, 9, 16, 17, 40, 129, 300):
             assert np.array_equal(rows_of(wb, n, M, **kw), full[:M]), f"bf16 weights M={M} {kw}"
     wf.free(), wb.free(), da.free()
+
