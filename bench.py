@@ -75,6 +75,54 @@ def time_steps(sess, step, steps: int, warmup: int):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def cpu_info() -> dict:
+    """The host CPU the baseline runs on: model, CPUs in this process's affinity mask, the threads used, and
+    the micro-kernels the baseline's start-up probe picked (AVX-512 only when >5% faster than AVX2, VNNI int8
+    when present: kernels/gemm/ukernel_amd64.go:65-93, kernels/gemm/qkernel_pick_amd64.go:18)."""
+    import oracle
+
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    affinity = len(os.sched_getaffinity(0))
+    # all CPUs this process may run on (GOMAXPROCS = every core: the reference's INGOT_WORKERS=nproc), unless
+    # the host declares a smaller CPU share for this job through OMP_NUM_THREADS
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(affinity, share) if share > 0 else affinity
+    rule = (f"OMP_NUM_THREADS={share} (this job's CPU share) of {affinity} CPUs in the affinity mask"
+            if 0 < share < affinity else f"every CPU in the affinity mask ({affinity})")
+    kernel, vnni = oracle.base_active_kernel()
+    return {"model": model, "affinity_cpus": affinity, "threads": threads, "threads_rule": rule,
+            "f32_kernel": kernel, "int8_kernel": "avx512-vnni" if vnni else "avx2-madd"}
+
+
+def cpu_time(fn, seconds: float):
+    """Median wall time of fn() over repeated calls after one warm-up call, for about `seconds`."""
+    fn()
+    times, t_end = [], time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end or len(times) >= 100000:
+            break
+    return float(np.median(times)), len(times)
+
+
+def cpu_entry(value, unit, info, kind_sample, **extra):
+    out = {"value": value, "unit": unit, "cores": info["threads"], "model": info["model"],
+           "affinity_cpus": info["affinity_cpus"], "threads_rule": info["threads_rule"], "kernels": f"{info['f32_kernel']} f32, {info['int8_kernel']} int8",
+           "kind": "port", "sample": kind_sample}
+    out.update(extra)
+    return out
+
+
 def event_ms(sess, fn, reps: int) -> float:
     """Average GPU time of fn() (HIP events on the session stream)."""
     fn()
@@ -109,6 +157,24 @@ class Dit:
     def step(self):
         for call in self.calls:
             call()
+
+    def default_math_report(self, steps: int, warmup: int):
+        """The same step under the library's default math for f32 A with bf16 weights: the f32-class hi/lo split
+        (A = hi + lo, both bf16, two MFMA products per tile), standing in for the reference's f32 math over
+        exactly widened bf16 weights (ops/matmul.go:77-137, kernels/gemm/gemm.go:920-962). It is what a caller
+        gets without GPUBF16."""
+        calls = [self.sess.prepare_gemm(self.a[k], w, y, self.M, act=act)
+                 for (k, n, _), w, y, act in zip(self.shapes, self.w, self.y, self.acts)]
+
+        def step():
+            for call in calls:
+                call()
+
+        ms = time_steps(self.sess, step, steps, warmup)
+        return {"TFLOPS": round(self.flops / (ms * 1e-3) / 1e12, 2), "ms_per_step": round(ms, 4),
+                "math": "default (bf16 hi/lo split of f32 A, f32 accumulate)",
+                "mfma_flops_per_step": 2 * self.flops,
+                "note": "value counts the step's algorithmic FLOPs; the hi/lo kind issues twice as many MFMA FLOPs"}
 
     def kernel_roofline(self):
         """The bf16 MFMA GEMM kernel alone: activations already bf16 (one launch per Gemm)."""
@@ -150,11 +216,11 @@ class Dit:
             s.gemm(a16[k], w, y, self.M, act=act, a_dtype=L.DT_BF16)
         s.sync()
 
-    def cpu_baseline(self, threads: int, seconds: float):
+    def cpu_baseline(self, info, seconds: float):
         import oracle
 
         rng = np.random.default_rng(20260405)
-        rows = 144  # one MC block of the reference's blocking, per GEMM
+        rows = 288  # two MC blocks of the reference's blocking, per GEMM
         packs = [oracle.PackedB(oracle.f32_to_bf16(normal32(rng, (n, k), 0.02)), trans_b=True, bf16=True)
                  for k, n, _ in self.shapes]
         a = {k: rng.normal(0, 1, (rows, k)).astype(np.float32) for k in (3072, 12288)}
@@ -162,20 +228,13 @@ class Dit:
 
         def once():
             for (k, n, tag), pb, o in zip(self.shapes, packs, outs):
-                oracle.base_sgemm(a[k], pb, gelu=tag.endswith("gelu"), threads=threads, out=o)
+                oracle.base_sgemm(a[k], pb, gelu=tag.endswith("gelu"), threads=info["threads"], out=o)
 
-        once()
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            once()
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= seconds or reps >= 10000:
-                break
+        t, reps = cpu_time(once, seconds)
         flops = sum(2.0 * rows * n * k for k, n, _ in self.shapes)
-        return {"value": round(flops * reps / el / 1e12, 4), "unit": "TFLOPS", "cores": threads, "kind": "port",
-                "sample": f"the 3 DiT GEMMs on {rows} of 4096 rows (bf16 weights widened per panel, f32 A), "
-                          f"{reps} reps in {el:.1f} s"}
+        return cpu_entry(round(flops / t / 1e12, 4), "TFLOPS", info,
+                         f"the 3 DiT GEMMs on {rows} of 4096 rows (bf16 weights widened per panel, f32 A); "
+                         f"median of {reps} passes", ms_per_step_full=round(t * 4096 / rows * 1e3, 2))
 
 
 class GemmRelu:
@@ -204,6 +263,24 @@ class GemmRelu:
         us = event_ms(self.sess, self.call, 200) * 1e3
         return {"value": round(self.flops / (us * 1e-6) / 1e12, 3), "unit": "TFLOPS", "us_per_call": round(us, 2),
                 "ms_per_step": round(ms, 4), "dtype": "f32"}
+
+    def cpu_baseline(self, info, seconds: float):
+        """The whole op on the host: packed-B f32 GEMM with the bias at the store, then the separate Relu node."""
+        import oracle
+
+        rng = np.random.default_rng(7)
+        a = rng.uniform(-1, 1, (self.M, self.K)).astype(np.float32)
+        pb = oracle.PackedB(rng.uniform(-1, 1, (self.N, self.K)).astype(np.float32), trans_b=True, bf16=False)
+        bias = rng.normal(0, 0.1, self.N).astype(np.float32)
+        y = np.empty((self.M, self.N), np.float32)
+
+        def once():
+            oracle.base_sgemm(a, pb, bias=bias, threads=info["threads"], out=y)
+            np.maximum(y, 0, out=y)
+
+        t, reps = cpu_time(once, seconds)
+        return cpu_entry(round(self.flops / t / 1e12, 4), "TFLOPS", info,
+                         f"the full Gemm+ReLU (128x256 . 512); median of {reps} calls", us_per_call=round(t * 1e6, 2))
 
 
 class Bert:
@@ -240,6 +317,26 @@ class Bert:
         return {"value": round(v, 2), "unit": "TFLOPS", "ms_per_step": round(ms, 4), "dtype": "f32",
                 "roofline_frac": round(v / PEAK["f32"], 4), "peak": PEAK["f32"]}
 
+    def cpu_baseline(self, info, seconds: float):
+        """The four projections at full size: packed-B f32 GEMMs with the bias at the store, GELU per finished
+        strip on FFN-up (SgemmPackedBEpi)."""
+        import oracle
+
+        rng = np.random.default_rng(1)
+        a = {k: rng.normal(0, 1, (self.M, k)).astype(np.float32) for k in (768, 3072)}
+        packs = [oracle.PackedB(rng.normal(0, 0.02, (k, n)).astype(np.float32), trans_b=False, bf16=False)
+                 for k, n, _ in self.shapes]
+        biases = [rng.normal(0, 0.02, n).astype(np.float32) for _, n, _ in self.shapes]
+        outs = [np.empty((self.M, n), np.float32) for _, n, _ in self.shapes]
+
+        def once():
+            for (k, n, gelu), pb, b, o in zip(self.shapes, packs, biases, outs):
+                oracle.base_sgemm(a[k], pb, bias=b, gelu=bool(gelu), threads=info["threads"], out=o)
+
+        t, reps = cpu_time(once, seconds)
+        return cpu_entry(round(self.flops / t / 1e12, 4), "TFLOPS", info,
+                         f"the 4 BERT projections at M = 1024; median of {reps} passes", ms_per_step=round(t * 1e3, 3))
+
 
 class Int8:
     name = "int8"
@@ -274,8 +371,28 @@ class Int8:
         tops = self.ops / (ms * 1e-3) / 1e12
         gbs = self.bytes / (ms * 1e-3) / 1e9
         return {"value": round(tops, 2), "unit": "TOPS", "ms_per_step": round(ms, 4), "dtype": "i8",
-                "GB_per_s": round(gbs, 1), "hbm_frac": round(gbs / PEAK["hbm"], 4),
+                "us_per_call": round(ms * 1e3, 2), "GB_per_s": round(gbs, 1), "hbm_frac": round(gbs / PEAK["hbm"], 4),
                 "mfma_frac": round(tops / PEAK["i8"], 4)}
+
+    def cpu_baseline(self, info, seconds: float):
+        """The full MatMulInteger (exact int32, VNNI when the host has it) then the per-column dequantisation
+        pass (the reference's separate DequantizeLinear node)."""
+        import oracle
+
+        rng = np.random.default_rng(3)
+        a = rng.integers(0, 256, (self.M, self.K)).astype(np.uint8)
+        bt = np.ascontiguousarray(rng.integers(-127, 128, (self.K, self.N)).astype(np.int8).T)
+        sc = (rng.uniform(0.001, 0.01, self.N).astype(np.float32) * np.float32(0.02)).astype(np.float32)
+        y = np.empty((self.M, self.N), np.float32)
+
+        def once():
+            yi = oracle.base_qgemm(a, bt, 128, threads=info["threads"])
+            np.multiply(yi.astype(np.float32), sc, out=y)
+
+        t, reps = cpu_time(once, seconds)
+        return cpu_entry(round(self.ops / t / 1e12, 4), "TOPS", info,
+                         f"the full MatMulInteger + DequantizeLinear; median of {reps} calls",
+                         us_per_call=round(t * 1e6, 1))
 
 
 class Decode:
@@ -318,13 +435,24 @@ class Decode:
         for call in calls:
             call()
 
+    def kernels(self, M):
+        """Which kernel each shape runs at this M (the routing of gemm_core: the decode GEMV for M <= 4, and
+        for M = 5..16 when N < 4096; the tiled GEMM otherwise)."""
+        return {f"{k}x{n}": "gemv" if M <= 4 or (M <= 16 and n < 4096) else "gemm" for k, n in self.shapes}
+
     def report(self):
         out = {}
         for M in (1, 4, 16):
             ms = time_steps(self.sess, lambda: self.step(M), 60, 10)
             gbs = self.bytes_step(M) / (ms * 1e-3) / 1e9
-            out[f"m{M}"] = {"GB_per_s": round(gbs, 1), "us_per_step": round(ms * 1e3, 2),
-                            "hbm_frac": round(gbs / PEAK["hbm"], 4)}
+            kern = self.kernels(M)
+            leg = {"GB_per_s": round(gbs, 1), "us_per_step": round(ms * 1e3, 2), "kernels": kern}
+            if all(v == "gemv" for v in kern.values()):
+                leg["hbm_frac"] = round(gbs / PEAK["hbm"], 4)
+            else:
+                # a decode-step rate (weight + activation bytes over the step), not one kernel's HBM roofline
+                leg["step_bytes_frac_of_hbm"] = round(gbs / PEAK["hbm"], 4)
+            out[f"m{M}"] = leg
         # per-shape kernel time at M=1 (events over rotated launches), after a
         # warm-up pass over every shape so the first one timed is not the one
         # that follows the M=16 leg
@@ -360,6 +488,23 @@ class Decode:
             for w in cp:
                 w.free()
         return out
+
+    def cpu_baseline(self, info, seconds: float):
+        """The M = 1 decode step on the host: the four bf16-weight GEMVs with a widening dot (GemvBF16)."""
+        import oracle
+
+        rng = np.random.default_rng(4)
+        xs = {k: rng.normal(0, 1, (1, k)).astype(np.float32) for k in (2048, 5632)}
+        ws = [oracle.f32_to_bf16(normal32(rng, (n, k), 0.02)) for k, n in self.shapes]
+
+        def once():
+            for (k, n), w in zip(self.shapes, ws):
+                oracle.base_gemv_bf16(xs[k], w, threads=info["threads"])
+
+        t, reps = cpu_time(once, seconds)
+        return cpu_entry(round(self.bytes_step(1) / t / 1e9, 2), "GB/s", info,
+                         f"the M = 1 decode step (4 GEMVs, 103 MB of bf16 weights); median of {reps} steps",
+                         us_per_step=round(t * 1e6, 1))
 
 
 class FfnGraph:
@@ -418,7 +563,9 @@ def main() -> int:
     ap.add_argument("--workload", default="dit", choices=["dit", "bert", "int8", "decode"])
     ap.add_argument("--no-extra", action="store_true", help="measure only the headline workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU-baseline time budget of the DiT leg")
+    ap.add_argument("--cpu-seconds-extra", type=float, default=3.0,
+                    help="CPU-baseline time budget of each other workload")
     ap.add_argument("--probe", nargs="?", const="dit", choices=["dit", "decode", "bert", "int8"],
                     help="counter probe for rocprofv3 --pmc: one calibration copy, then one launch of each DiT GEMM "
                          "(dit, the default) or one decode GEMV step at M = 1, 4, 16 (decode); bert: one launch of "
@@ -450,10 +597,12 @@ def main() -> int:
                                "global_batch": 4096, "parallelism": "none (1 GPU)"}})
         log(f"dit: {res['value']} TFLOPS, {ms:.3f} ms/step; kernel roofline")
         res["roofline"] = wl.kernel_roofline()
-        if not args.no_cpu_baseline:
-            threads = min(16, len(os.sched_getaffinity(0)))
-            log(f"dit: cpu baseline on {threads} threads")
-            res["cpu_baseline"] = wl.cpu_baseline(threads, args.cpu_seconds)
+        log("dit: default-math (hi/lo) step")
+        res["dit_default_math"] = wl.default_math_report(args.steps, args.warmup)
+        info = cpu_info() if not args.no_cpu_baseline else None
+        if info:
+            log(f"dit: cpu baseline on {info['threads']} threads ({info['model']})")
+            res["cpu_baseline"] = wl.cpu_baseline(info, args.cpu_seconds)
     else:
         wl = {"bert": Bert, "int8": Int8, "decode": Decode}[args.workload](sess, L)
         if args.workload == "decode":
@@ -472,8 +621,13 @@ def main() -> int:
             log(f"{cls.name}: measuring")
             w = cls(sess, L)
             extra[cls.name] = w.report(time_steps(sess, w.step, 50, 10))
+            if info:
+                extra[cls.name]["cpu_baseline"] = w.cpu_baseline(info, args.cpu_seconds_extra)
         log("decode: measuring")
-        extra["decode"] = Decode(sess, L).report()
+        dec = Decode(sess, L)
+        extra["decode"] = dec.report()
+        if info:
+            extra["decode"]["cpu_baseline"] = dec.cpu_baseline(info, args.cpu_seconds_extra)
         log("ffn graph: measuring")
         extra["ffn_graph"] = FfnGraph(sess, L).report()
         res["workloads"] = extra

@@ -101,6 +101,8 @@ __device__ __forceinline__ void wait_dma_groups(int groups) {
         case 3: waitcnt_vm<(NS > 3 ? 3 : 0) * G>(); break;
         case 4: waitcnt_vm<(NS > 4 ? 4 : 0) * G>(); break;
         case 5: waitcnt_vm<(NS > 5 ? 5 : 0) * G>(); break;
+        case 6: waitcnt_vm<(NS > 6 ? 6 : 0) * G>(); break;
+        case 7: waitcnt_vm<(NS > 7 ? 7 : 0) * G>(); break;
         default: waitcnt_vm<0>(); break;
     }
 }
@@ -413,8 +415,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(typename Kernel
                     f[e] = (float)wrap_add(v[e], -q.dq_zp) * sc[e];
                 }
                 if (full && vec_ok) {
-                    if (q.yi) *(i32x4_t*)(q.yi + o) = i32x4_t{v[0], v[1], v[2], v[3]};
-                    if (q.yf) *(f32x4_t*)(q.yf + o) = f32x4_t{f[0], f[1], f[2], f[3]};
+                    // non-temporal: the int32 / f32 outputs are 4× the operand
+                    // bytes, and leaving them dirty in L2 makes the end of the
+                    // kernel wait for their write-back (on MI355X the 1024 × 768
+                    // → 3072 MatMulInteger + dequant took 9.0 µs per call with
+                    // plain stores, 7.2–7.5 with these)
+                    if (q.yi) __builtin_nontemporal_store(i32x4_t{v[0], v[1], v[2], v[3]}, (i32x4_t*)(q.yi + o));
+                    if (q.yf) __builtin_nontemporal_store(f32x4_t{f[0], f[1], f[2], f[3]}, (f32x4_t*)(q.yf + o));
                 } else {
                     for (int e = 0; e < 4 && n + e < p.N; ++e) {
                         if (q.yi) q.yi[o + e] = v[e];

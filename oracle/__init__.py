@@ -82,6 +82,8 @@ def baseline() -> C.CDLL:
         B.base_sgemm_packed.argtypes = [_I64, _P, _I64, _P, _P, _I64, _P, C.c_int, C.c_int]
         B.base_gemv_bf16.argtypes = [_I64, _I64, _I64, _P, _P, _P, C.c_int]
         B.base_qgemm.argtypes = [_I64, _I64, _I64, _P, C.c_int32, _P, _P, C.c_int]
+        B.base_active_kernel.restype = C.c_char_p
+        B.base_active_kernel.argtypes = [C.POINTER(C.c_int)]
         _base = B
     return _base
 
@@ -343,3 +345,10 @@ def base_qgemm(a: np.ndarray, bt: np.ndarray, za: int, threads=1) -> np.ndarray:
     y = np.empty((m, n), np.int32)
     baseline().base_qgemm(m, n, k, _p(a), za, _p(bt), _p(y), threads)
     return y
+
+
+def base_active_kernel():
+    """(micro-kernel name, VNNI int8 kernel in use) as the baseline's start-up probe picked them."""
+    v = C.c_int()
+    name = baseline().base_active_kernel(C.byref(v)).decode()
+    return name, bool(v.value)
