@@ -200,7 +200,87 @@ class Dit:
                 "frac": round(achieved / PEAK["bf16"], 4), "traffic": measured_traffic(),
                 "kernel": "gemm_kernel<bf16> (256x192 for QKV and MLP-down, 256x256 for MLP-up)",
                 "avg_launch_us": round(ms * 1e3, 2),
-                "flops_per_launch": flops}
+                "flops_per_launch": flops,
+                "zero_operands": self.zero_operand_rate()}
+
+    def zero_operand_rate(self):
+        """The same kernels, shapes and launch order on all-zero A and weights. The schedule, the data movement
+        and the instruction stream are identical; only the operand bits differ, so the gap to the random-data
+        rate is what the MFMA arrays' data-dependent power costs (the clock drops under the power limit)."""
+        L, s = self.L, self.sess
+        a16 = {k: s.empty(L.DT_BF16, (self.M, k)) for k in (3072, 12288)}
+        for t in a16.values():
+            s.memset(t, 0)
+        ws = [s.upload_weight(np.zeros((n, k), np.float32), trans=True, pack_dtype=L.DT_BF16)
+              for k, n, _ in self.shapes]
+        calls = [s.prepare_gemm(a16[k], w, y, self.M, act=act, a_dtype=L.DT_BF16)
+                 for (k, n, _), w, y, act in zip(self.shapes, ws, self.y, self.acts)]
+
+        def launches():
+            for call in calls:
+                call()
+
+        ms = event_ms(s, launches, 10) / len(self.shapes)
+        for t in a16.values():
+            t.free()
+        for w in ws:
+            w.free()
+        achieved = self.flops / len(self.shapes) / (ms * 1e-3) / 1e12
+        return {"achieved": round(achieved, 1), "frac": round(achieved / PEAK["bf16"], 4),
+                "avg_launch_us": round(ms * 1e3, 2)}
+
+    def compare_hipblaslt(self, reps: int = 20):
+        """The bf16 GEMM kernel against hipBLASLt (torch.mm with bf16 operands and f32 output, the same output
+        type as the Gemm op) on the same operand values, per DiT GEMM: each side timed with HIP events over
+        `reps` back-to-back launches on its own stream, four times, alternating (the first rounds run while
+        the clock settles, so the minimum is compared). Neither includes the activation pack. Prints one
+        JSON line per GEMM."""
+        import torch
+
+        L, s = self.L, self.sess
+        rng = np.random.default_rng(20260405)
+        for (k, n, tag), act in zip(self.shapes, self.acts):
+            a = rng.normal(0, 1, (self.M, k)).astype(np.float32)
+            w = normal32(rng, (n, k), 0.02)
+            da = s.to_device(a)
+            a16 = s.empty(L.DT_BF16, (self.M, k))
+            s.cast_bf16(da, a16)
+            wt = s.upload_weight(w, trans=True, pack_dtype=L.DT_BF16)
+            y = s.empty(L.DT_F32, (self.M, n))
+            call = s.prepare_gemm(a16, wt, y, self.M, a_dtype=L.DT_BF16)
+            ta = torch.from_numpy(a).to("cuda").to(torch.bfloat16)
+            tw = torch.from_numpy(w).to("cuda").to(torch.bfloat16)
+
+            def blas():
+                return torch.mm(ta, tw.t(), out_dtype=torch.float32)
+
+            def blas_ms():
+                for _ in range(3):
+                    blas()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(reps):
+                    blas()
+                e1.record()
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1) / reps
+
+            ours, theirs = [], []
+            for _ in range(4):
+                ours.append(event_ms(s, call, reps) * 1e3)
+                theirs.append(blas_ms() * 1e3)
+            flops = 2.0 * self.M * n * k
+            print(json.dumps({"gemm": f"{tag} {self.M}x{k}x{n}", "ours_us": [round(v, 1) for v in ours],
+                              "hipblaslt_us": [round(v, 1) for v in theirs],
+                              "ours_tflops": round(flops / (min(ours) * 1e-6) / 1e12, 1),
+                              "hipblaslt_tflops": round(flops / (min(theirs) * 1e-6) / 1e12, 1),
+                              "epilogue": "none on either side"}),
+                  flush=True)
+            for t in (da, a16, y):
+                t.free()
+            wt.free()
+            del ta, tw
 
     def probe(self):
         """One plain copy of PROBE_COPY_BYTES (counter calibration), then one launch of each GEMM."""
@@ -566,19 +646,30 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU-baseline time budget of the DiT leg")
     ap.add_argument("--cpu-seconds-extra", type=float, default=3.0,
                     help="CPU-baseline time budget of each other workload")
-    ap.add_argument("--probe", nargs="?", const="dit", choices=["dit", "decode", "bert", "int8"],
+    ap.add_argument("--probe", nargs="?", const="dit", choices=["dit", "decode", "bert", "int8", "hipblaslt"],
                     help="counter probe for rocprofv3 --pmc: one calibration copy, then one launch of each DiT GEMM "
                          "(dit, the default) or one decode GEMV step at M = 1, 4, 16 (decode); bert: one launch of "
-                         "each BERT f32 projection; int8: one calibration copy, then one MatMulInteger + dequant call")
+                         "each BERT f32 projection; int8: one calibration copy, then one MatMulInteger + dequant call; "
+                         "hipblaslt: the DiT GEMM kernel against hipBLASLt on the same operands (one JSON line each)")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU (the path has no multi-GPU component); run with --gpus 1")
         return 2
 
+    if args.probe == "hipblaslt":
+        # torch's HIP runtime is loaded and initialised before the library's (started the other way round,
+        # torch finds no GPU)
+        import torch
+
+        torch.cuda.init()
     from ingot_amd import Session
     from ingot_amd import _lib as L
 
     sess = Session(0)
+    if args.probe == "hipblaslt":
+        Dit(sess, L).compare_hipblaslt()
+        sess.close()
+        return 0
     if args.probe:
         {"dit": Dit, "decode": Decode, "bert": Bert, "int8": Int8}[args.probe](sess, L).probe()
         sess.close()
