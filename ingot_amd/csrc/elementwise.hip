@@ -1,6 +1,8 @@
 // Memory-bound helper kernels: weight and activation packing, DequantizeLinear,
 // the standalone activation / bias pass, the f32 → bf16 cast and fills.
 
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace ingot {
@@ -152,6 +154,49 @@ __global__ void pack_a_kernel(const void* src, int src_dt, int64_t lda, int tran
     }
 }
 
+// The common activation pack — f32 rows already dense in whole k-tiles (lda = k = kl, one batch
+// item), to bf16 (or the hi/lo planes) — as a flat stream: each thread converts U groups of 8
+// elements per step, all U loads issued before any conversion, over a grid of a few workgroups
+// per CU (grid-stride), so that the copy runs at streaming rate instead of one small workgroup
+// per 2048 elements.
+template <int KD, int U>
+__global__ __launch_bounds__(256) void pack_a_flat_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
+                                                          int64_t groups, int64_t plane) {
+    const int64_t stride = (int64_t)gridDim.x * 256 * U;
+    for (int64_t g0 = (int64_t)blockIdx.x * 256 * U + threadIdx.x; g0 < groups; g0 += stride) {
+        f32x4_t v[U][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t g = g0 + (int64_t)u * 256;
+            if (g < groups) {
+                v[u][0] = __builtin_nontemporal_load((const f32x4_t*)(src + g * 8));
+                v[u][1] = __builtin_nontemporal_load((const f32x4_t*)(src + g * 8 + 4));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t g = g0 + (int64_t)u * 256;
+            if (g >= groups) continue;
+            uint16_t h[8], l[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = v[u][e >> 2][e & 3];
+                if (KD == KIND_BF16X2)
+                    split_bf16(x, h[e], l[e]);
+                else
+                    h[e] = f32_to_bf16(x);
+            }
+            i32x4_t out;
+            __builtin_memcpy(&out, h, 16);
+            *(i32x4_t*)(dst + g * 8) = out;
+            if (KD == KIND_BF16X2) {
+                __builtin_memcpy(&out, l, 16);
+                *(i32x4_t*)(dst + plane + g * 8) = out;
+            }
+        }
+    }
+}
+
 __global__ void dequant_kernel(const void* x, int x_dt, int64_t n, const float* scale, int64_t n_scale, int64_t inner,
                                const void* zp, int zp_dt, int64_t n_zp, float* y) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
@@ -204,6 +249,19 @@ hipError_t launch_pack_a(const void* src, int src_dtype, int64_t lda, int trans,
                          int64_t src_stride, void* dst, GemmKind dst_kind, int64_t kl, int64_t dst_stride, int batch,
                          hipStream_t st) {
     const int epc = dst_kind == KIND_F32 ? 4 : (dst_kind == KIND_I8 ? 16 : 8);
+    if ((dst_kind == KIND_BF16 || dst_kind == KIND_BF16X2) && src_dtype == INGOT_DT_F32 && !trans && batch == 1 &&
+        lda == k && kl == k && k % 8 == 0 && (((uintptr_t)src) & 15) == 0 && (((uintptr_t)dst) & 15) == 0) {
+        const int64_t groups = m * k / 8;
+        const int64_t need = (groups + 256 * 4 - 1) / (256 * 4);
+        const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(need, 2048));
+        if (dst_kind == KIND_BF16)
+            hipLaunchKernelGGL((pack_a_flat_kernel<KIND_BF16, 4>), dim3(grid), dim3(256), 0, st, (const float*)src,
+                               (uint16_t*)dst, groups, m * kl);
+        else
+            hipLaunchKernelGGL((pack_a_flat_kernel<KIND_BF16X2, 4>), dim3(grid), dim3(256), 0, st, (const float*)src,
+                               (uint16_t*)dst, groups, m * kl);
+        return hipGetLastError();
+    }
     const int64_t chunks = kl / epc;
     dim3 grid((unsigned)((chunks + 255) / 256), (unsigned)(m < 65535 ? (m > 0 ? m : 1) : 65535), batch);
     const int64_t plane = m * kl;
