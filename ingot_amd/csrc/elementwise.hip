@@ -249,8 +249,11 @@ hipError_t launch_pack_a(const void* src, int src_dtype, int64_t lda, int trans,
                          int64_t src_stride, void* dst, GemmKind dst_kind, int64_t kl, int64_t dst_stride, int batch,
                          hipStream_t st) {
     const int epc = dst_kind == KIND_F32 ? 4 : (dst_kind == KIND_I8 ? 16 : 8);
+    // (large activations only: at decode sizes the per-row grid below spreads the few rows over more CUs;
+    // M = 16, K = 2048 took 5.4 us flat against 3.7)
     if ((dst_kind == KIND_BF16 || dst_kind == KIND_BF16X2) && src_dtype == INGOT_DT_F32 && !trans && batch == 1 &&
-        lda == k && kl == k && k % 8 == 0 && (((uintptr_t)src) & 15) == 0 && (((uintptr_t)dst) & 15) == 0) {
+        lda == k && kl == k && k % 8 == 0 && m * k >= ((int64_t)1 << 22) && (((uintptr_t)src) & 15) == 0 &&
+        (((uintptr_t)dst) & 15) == 0) {
         const int64_t groups = m * k / 8;
         const int64_t need = (groups + 256 * 4 - 1) / (256 * 4);
         const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(need, 2048));

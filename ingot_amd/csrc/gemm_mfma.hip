@@ -149,8 +149,18 @@ template <> struct KernelArgs<KIND_I8> { typedef GemmArgsQ type; };
 
 template <int KD, int BM, int BN, int WGM, int WGN, int NS>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(typename KernelArgs<KD>::type p) {
+    // The hi/lo kind (A = hi + lo, two bf16 planes) sums each k-tile in one
+    // order on every tile: hi first half, hi second half, lo first half, lo
+    // second half. Tiles over 128 rows run it as a bf16 GEMM over twice the
+    // k-tiles (SPLITK: virtual k-tile 2j is k-tile j of the hi plane, 2j + 1 the
+    // same k-tile of the lo plane, both against weight k-tile j), so one
+    // activation plane per LDS stage and the bf16 kind's ring; smaller tiles
+    // hold both planes in a stage (AP = 2) and multiply in the same order, so a
+    // k-tile's weight bytes are loaded once. Every tile of the kind gives the
+    // same sums.
     constexpr bool SPLIT = KD == KIND_BF16X2;
-    constexpr int AP = SPLIT ? 2 : 1;  // activation planes
+    constexpr bool SPLITK = SPLIT && BM > 128;
+    constexpr int AP = SPLIT && !SPLITK ? 2 : 1;  // activation planes per LDS stage
     constexpr int NW = WGM * WGN;      // waves per workgroup
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 16, TN = WN / 16;
@@ -222,15 +232,19 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(typename Kernel
     // host keeps row offsets below 2^31), so its load fetches nothing and
     // writes zeros: the pipeline below issues one DMA group per k-tile
     // unconditionally.
-    const int KT = p.kt;
+    const int KT = SPLITK ? 2 * p.kt : p.kt;
     auto dma = [&](char* st, int kt) {
-        const uint32_t kofs = kt < KT ? (uint32_t)kt * KTILE_BYTES : 0x80000000u;
+        // plane offsets stay below 2^31 with the rest of the row offset (the host bounds the extent
+        // of both planes), so a past-the-end k-tile still lands out of range
+        const int kr = SPLITK ? kt >> 1 : kt;
+        const uint32_t aofs = SPLITK ? (uint32_t)(kt & 1) * (uint32_t)p.a_plane_bytes : 0u;
+        const uint32_t kofs = kt < KT ? (uint32_t)kr * KTILE_BYTES : 0x80000000u;
 #pragma unroll
         for (int pl = 0; pl < AP; ++pl)
 #pragma unroll
             for (int j = 0; j < IA; ++j) {
                 const int r = (j * NW + wave) * 8;
-                const uint32_t row = (uint32_t)((m0 + r) * p.lda_bytes + pl * p.a_plane_bytes) + kofs;
+                const uint32_t row = (uint32_t)((m0 + r) * p.lda_bytes) + aofs + (uint32_t)pl * (uint32_t)p.a_plane_bytes + kofs;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, LDS_AS(st + (pl * BM + r) * KTILE_BYTES), 16,
                                                          voff_a[(r >> 3) & 1] + row, 0, 0, 0);
             }
@@ -273,13 +287,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(typename Kernel
 #pragma unroll
         for (int j = 0; j < TN; ++j) fb[j] = *(const i32x4_t*)(st + b_off[s] + j * 16 * KTILE_BYTES);
     };
-    auto mma_all = [&](const FragA& fa, const FragB& fb) {
+    // the products of one activation plane and one half k-tile
+    auto mma_plane = [&](const i32x4_t (&fa)[TM], const FragB& fb) {
 #pragma unroll
-        for (int pl = 0; pl < AP; ++pl)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) mma16<KD>(acc[i][j], fb[j], fa[pl][i]);
+            for (int j = 0; j < TN; ++j) mma16<KD>(acc[i][j], fb[j], fa[i]);
     };
 
     // Software pipeline over k-tiles: an NS-stage LDS ring filled by DMA NS
@@ -297,7 +310,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(typename Kernel
     // the half's last MFMA.
     constexpr int G = AP * IA + IB;                               // DMA instructions per wave per k-tile
     constexpr int NFR = AP * TM + TN;                             // LDS fragment reads per half
-    constexpr int NMF = (KD == KIND_F32 ? 4 : 1) * AP * TM * TN;  // MFMAs per half
+    // MFMAs per half of the loop body: with both planes in a stage the first
+    // half multiplies the hi plane's two half k-tiles, the second the lo plane's
+    constexpr int NMF0 = (KD == KIND_F32 ? 4 : 1) * AP * TM * TN;
+    constexpr int NMF1 = NMF0;
     FragA fa0, fa1;
     FragB fb0, fb1;
     // The epilogue terms: raw loads issued right after k-tile 0's DMA, the
@@ -350,16 +366,30 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_kernel(typename Kernel
         char* cur = lds + st * SSTRIDE;
         const int st1 = st + 1 == NS ? 0 : st + 1;
         read_frags(cur, 1, fa1, fb1);
-        mma_all(fa0, fb0);
-        interleave<NMF, 0, NFR>();
+        mma_plane(fa0[0], fb0);
+        if constexpr (AP == 2) mma_plane(fa1[0], fb1);
+        interleave<NMF0, 0, NFR>();
         __builtin_amdgcn_sched_barrier(0);
         wait_dma_groups<G, NS>(NS - 2);
         kloop_barrier();  // cur fully read by every wave; k-tile kt+1 landed
         __builtin_amdgcn_sched_barrier(0);
         dma(cur, kt + NS);
-        read_frags(lds + st1 * SSTRIDE, 0, fa0, fb0);  // after the last k-tile: unused
-        mma_all(fa1, fb1);
-        interleave<NMF, G, NFR>();
+        if constexpr (AP == 2) {
+            // lo first half (kept from before the refill), then lo second half
+            i32x4_t lo0[TM];
+            FragB b0;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) lo0[i] = fa0[1][i];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b0[j] = fb0[j];
+            read_frags(lds + st1 * SSTRIDE, 0, fa0, fb0);  // after the last k-tile: unused
+            mma_plane(lo0, b0);
+            mma_plane(fa1[1], fb1);
+        } else {
+            read_frags(lds + st1 * SSTRIDE, 0, fa0, fb0);  // after the last k-tile: unused
+            mma_plane(fa1[0], fb1);
+        }
+        interleave<NMF1, G, NFR>();
         __builtin_amdgcn_sched_barrier(0);
         st = st1;
     }
@@ -558,8 +588,6 @@ const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128
 // on the BERT projections, so weighted 0.8.
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}, {32, 96, 4, 0.97f},
                                {32, 32, 4, 0.80f}};
-const GemmConfig kBF16X2Cfgs[] = {{128, 128, 1, 1.00f}, {128, 64, 2, 0.85f}, {64, 64, 3, 0.60f}, {32, 32, 3, 0.60f, true},
-                                  {64, 64, 1, 1.00f, true}};
 // int8 64×96: two tiles per CU at M = 1024, N = 3072 (512 tiles) instead of three 64×64 ones:
 // 9.0 vs 9.6 µs on MI355X (fewer panel re-reads through L2); 128×96, 32×96, 64×128,
 // 64×192, 32-row tiles (32×32 to 32×128) and deeper rings were slower there.
@@ -592,7 +620,8 @@ int gemm_configs(GemmKind kind, const GemmConfig** out) {
         case KIND_BF16: *out = kBF16Cfgs; return (int)(sizeof(kBF16Cfgs) / sizeof(kBF16Cfgs[0]));
         case KIND_F32: *out = kF32Cfgs; return (int)(sizeof(kF32Cfgs) / sizeof(kF32Cfgs[0]));
         case KIND_I8: *out = kI8Cfgs; return (int)(sizeof(kI8Cfgs) / sizeof(kI8Cfgs[0]));
-        case KIND_BF16X2: *out = kBF16X2Cfgs; return (int)(sizeof(kBF16X2Cfgs) / sizeof(kBF16X2Cfgs[0]));
+        // the hi/lo kind runs the bf16 kernels over twice the k-tiles: the same tiles
+        case KIND_BF16X2: *out = kBF16Cfgs; return (int)(sizeof(kBF16Cfgs) / sizeof(kBF16Cfgs[0]));
     }
     return 0;
 }
@@ -616,11 +645,15 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
             break;
         case KIND_BF16X2:
             switch (cfg) {
-                case 0: return launch_one<KIND_BF16X2, 128, 128, 2, 2, 2>(a, batch, st);
-                case 1: return launch_one<KIND_BF16X2, 128, 64, 2, 2, 2>(a, batch, st);
-                case 2: return launch_one<KIND_BF16X2, 64, 64, 2, 2, 2>(a, batch, st);
-                case 3: return launch_one<KIND_BF16X2, 32, 32, 2, 2, 4>(a, batch, st);
-                case 4: return launch_one<KIND_BF16X2, 64, 64, 2, 2, 4>(a, batch, st);
+                case 0: return launch_one<KIND_BF16X2, 256, 256, 4, 2, 2>(a, batch, st);
+                case 1: return launch_one<KIND_BF16X2, 256, 192, 4, 2, 2>(a, batch, st);
+                case 2: return launch_one<KIND_BF16X2, 128, 128, 2, 2, 2>(a, batch, st);
+                case 3: return launch_one<KIND_BF16X2, 128, 64, 2, 2, 2>(a, batch, st);
+                case 4: return launch_one<KIND_BF16X2, 64, 64, 2, 2, 2>(a, batch, st);
+                case 5: return launch_one<KIND_BF16X2, 192, 256, 2, 4, 2>(a, batch, st);
+                case 6: return launch_one<KIND_BF16X2, 64, 96, 2, 2, 2>(a, batch, st);
+                case 7: return launch_one<KIND_BF16X2, 32, 32, 2, 2, 4>(a, batch, st);
+                case 8: return launch_one<KIND_BF16X2, 64, 64, 2, 2, 4>(a, batch, st);
             }
             break;
         case KIND_F32:
