@@ -586,8 +586,13 @@ const GemmConfig kBF16Cfgs[] = {{256, 256, 1, 1.00f}, {256, 192, 1, 0.95f}, {128
 // 6.2 µs per call on MI355X; at M = 32, N = 6144, K = 2048 (64 k-tiles) the ring
 // depth matters: 14.2 µs with four stages, 26.8 with two. 6–12% slower than 32×96
 // on the BERT projections, so weighted 0.8.
+// f32 32×96 with a four-stage ring, when every tile is resident at once (one
+// per CU): the BERT FFN-down (M = 1024, N = 768, K = 3072, 96 k-tiles, one
+// wave per SIMD, so nothing else covers a k-tile's DMA round trip) took 41.6
+// instead of 45.0 µs on MI355X; at three tiles per CU the two-stage ring stays
+// ahead (FFN-up 41.3 vs 43.7), and six stages were slower again (42.1).
 const GemmConfig kF32Cfgs[] = {{128, 128, 2, 0.90f}, {128, 64, 3, 0.95f}, {64, 64, 4, 1.00f}, {32, 96, 4, 0.97f},
-                               {32, 32, 4, 0.80f}};
+                               {32, 32, 4, 0.80f},   {32, 96, 2, 0.98f, true}};
 // int8 64×96: two tiles per CU at M = 1024, N = 3072 (512 tiles) instead of three 64×64 ones:
 // 9.0 vs 9.6 µs on MI355X (fewer panel re-reads through L2); 128×96, 32×96, 64×128,
 // 64×192, 32-row tiles (32×32 to 32×128) and deeper rings were slower there.
@@ -663,6 +668,7 @@ hipError_t launch_gemm(GemmKind kind, int cfg, const GemmArgs& a, int batch, hip
                 case 2: return launch_one<KIND_F32, 64, 64, 2, 2, 2>(a, batch, st);
                 case 3: return launch_one<KIND_F32, 32, 96, 2, 2, 2>(a, batch, st);
                 case 4: return launch_one<KIND_F32, 32, 32, 2, 2, 4>(a, batch, st);
+                case 5: return launch_one<KIND_F32, 32, 96, 2, 2, 4>(a, batch, st);
             }
             break;
         case KIND_I8:

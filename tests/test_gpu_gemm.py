@@ -299,7 +299,7 @@ def test_gemv_epilogue(sess, m):
 # ragged edges in M, N and K, with a bias and an activation in the epilogue
 # (int8: the column-sum correction and fused dequantisation). Indices follow the
 # configuration tables of gemm_mfma.hip.
-GEMM_CFGS = {"f32": range(5), "bf16": range(9), "bf16x2": range(9), "i8": range(6)}
+GEMM_CFGS = {"f32": range(6), "bf16": range(9), "bf16x2": range(9), "i8": range(6)}
 
 
 @pytest.mark.parametrize("kind,cfg", [(k, c) for k, r in GEMM_CFGS.items() for c in r])
