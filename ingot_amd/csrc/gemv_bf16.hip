@@ -136,6 +136,50 @@ __global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemvArgs p) {
 
 }  // namespace
 
+// A wave's R·MM sums (acc[r][m]: row row0 + r of W times row m of x), each
+// held as 64 lane partials, added by a butterfly over lane distances 32, 16,
+// ..., 1 and stored through the epilogue. While more than one sum is left per
+// lane, each step halves them: the lane keeps the upper half if its bit of the
+// distance is set, else the lower half, and adds its partner's copy of the half
+// it keeps (partner = lane ^ distance keeps the other). Every sum is formed by
+// exactly the pairings of a full butterfly, own partial first, so the result
+// is bit-identical to one, with V − 1 + log2(64 / V) exchanges instead of 6·V.
+// Sum j (= r·MM + m) ends in the lanes whose bits 5, 4, ... (one per halving)
+// spell j; the one with the other bits clear stores it.
+template <int R, int MM, typename A>
+__device__ __forceinline__ void reduce_store(float (&acc)[R][MM], int lane, int row0, const A& p) {
+    constexpr int V = R * MM;
+    static_assert((V & (V - 1)) == 0 && V <= 64, "R·MM must be a power of two");
+    float v[V];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) v[r * MM + m] = acc[r][m];
+    int j = 0;  // index of the first sum this lane still holds
+#pragma unroll
+    for (int c = V, off = 32; off > 0; off >>= 1) {
+        if (c > 1) {
+            const bool up = (lane & off) != 0;
+            c >>= 1;
+#pragma unroll
+            for (int i = 0; i < c; ++i) {
+                const float keep = up ? v[i + c] : v[i];
+                const float give = up ? v[i] : v[i + c];
+                v[i] = keep + __shfl_xor(give, off);
+            }
+            j = 2 * j + (up ? 1 : 0);
+        } else {
+            v[0] += __shfl_xor(v[0], off);
+        }
+    }
+    constexpr int SPLITS = V == 1 ? 0 : (V == 2 ? 1 : (V == 4 ? 2 : (V == 8 ? 3 : (V == 16 ? 4 : (V == 32 ? 5 : 6)))));
+    // the halving steps used lane bits 5 .. 6 − SPLITS; the store lane has the rest clear
+    if ((lane & ((64 >> SPLITS) - 1)) != 0) return;
+    const int r = j / MM, m = j % MM;
+    const int n = row0 + r;
+    if (n < p.N && m < p.M) store_y(p.y, (int64_t)m * p.ldy + n, epi_apply(p.epi, v[0], m, n), p.epi);
+}
+
 // ---- M <= 4: rows streamed whole by VALU FMAs ----
 // A wave owns R weight rows and walks K in 512-wide chunks: lane l reads the
 // 16 bytes at k = c·512 + 8l of each row (1 KiB contiguous per row per load
@@ -210,46 +254,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_rows_kernel(A p) {
                 }
             }
     }
-    // The 64 lane partials of the R·MM sums, added by a butterfly over lane
-    // distances 32, 16, ..., 1. While more than one sum is left per lane, each
-    // step halves them: the lane keeps the upper half if its bit of the
-    // distance is set, else the lower half, and adds its partner's copy of the
-    // half it keeps (partner = lane ^ distance keeps the other). Every sum is
-    // formed by exactly the pairings of a full butterfly, own partial first,
-    // so the result is bit-identical to one, with V − 1 + log2(64 / V)
-    // exchanges instead of 6·V. Sum j (= r·MM + m) ends in the lanes whose
-    // bits 5, 4, ... (one per halving) spell j; the one with the other bits
-    // clear stores it.
-    constexpr int V = R * MM;
-    static_assert((V & (V - 1)) == 0 && V <= 64, "R·MM must be a power of two");
-    float v[V];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < MM; ++m) v[r * MM + m] = acc[r][m];
-    int j = 0;  // index of the first sum this lane still holds
-#pragma unroll
-    for (int c = V, off = 32; off > 0; off >>= 1) {
-        if (c > 1) {
-            const bool up = (lane & off) != 0;
-            c >>= 1;
-#pragma unroll
-            for (int i = 0; i < c; ++i) {
-                const float keep = up ? v[i + c] : v[i];
-                const float give = up ? v[i] : v[i + c];
-                v[i] = keep + __shfl_xor(give, off);
-            }
-            j = 2 * j + (up ? 1 : 0);
-        } else {
-            v[0] += __shfl_xor(v[0], off);
-        }
-    }
-    constexpr int SPLITS = V == 1 ? 0 : (V == 2 ? 1 : (V == 4 ? 2 : (V == 8 ? 3 : (V == 16 ? 4 : (V == 32 ? 5 : 6)))));
-    // the halving steps used lane bits 5 .. 6 − SPLITS; the store lane has the rest clear
-    if ((lane & ((64 >> SPLITS) - 1)) != 0) return;
-    const int r = j / MM, m = j % MM;
-    const int n = row0 + r;
-    if (n < p.N && m < p.M) store_y(p.y, (int64_t)m * p.ldy + n, epi_apply(p.epi, v[0], m, n), p.epi);
+    reduce_store<R, MM>(acc, lane, row0, p);
 }
 
 template <int R, int MM, int WPB = 4, int CHX = 0, typename A = GemvArgs>
