@@ -638,3 +638,34 @@ def test_m_invariance(sess):
             assert np.array_equal(rows_of(wb, n, M, **kw), full[:M]), f"bf16 weights M={M} {kw}"
     wf.free(), wb.free(), da.free()
 
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_hilo_random_shapes_and_row_invariance(sess, seed):
+    """The default math for f32 A × bf16 W (hi/lo planes) on random shapes: large-tile launches (two
+    activation planes as a doubled k-tile sequence) and small-tile ones (both planes per LDS stage) are held
+    to the reference's f32-class bound (relative 1e-5·sqrt(K), ops/gemm_bf16_optest_test.go:57) against the
+    float64 oracle with a bias and GELU; and the rows the smaller call shares with the larger one are
+    bit-identical (both tile families multiply each k-tile hi first half, hi second half, lo first half, lo
+    second half), as kernels/gemm/minvariance_test.go:21 asks of a GEMM."""
+    rng = np.random.default_rng(9000 + seed)
+    m = int(rng.integers(300, 1400))
+    n = int(rng.integers(4096, 7000)) if seed % 3 == 0 else int(rng.integers(1, 1500))
+    k = int(rng.integers(1, 2100))
+    m_small = int(rng.integers(17, 65))
+    announce(f"hi/lo random seed={seed} m={m} m_small={m_small} n={n} k={k}")
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k), 0.05, "normal")
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    da, db = sess.to_device(a), sess.to_device(bias)
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    kw = dict(beta=1.0, c=db, c_mode=L.C_ROW, act=L.ACT_GELU_ERF)
+    got = run_gemm(sess, da, w, m, **kw)
+    rows = np.unique(np.concatenate([np.arange(min(m, 40)), rng.integers(0, m, 60)]))
+    want = oracle.gemm(np.ascontiguousarray(a[rows]), wb, trans_b=True, b_dtype=oracle.BF16, beta=1.0, c=bias,
+                       c_mode=L.C_ROW, act_code=L.ACT_GELU_ERF)
+    rel = np.max(np.abs(got[rows] - want) / (1 + np.abs(want)))
+    assert rel <= 1e-5 * math.sqrt(max(k, 1)), f"relative error {rel:.3e}"
+    small = run_gemm(sess, da, w, m_small, **kw)
+    assert np.array_equal(small, got[:m_small]), f"rows differ between M={m_small} and M={m}"
+    w.free(), da.free(), db.free()
