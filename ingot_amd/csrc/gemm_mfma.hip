@@ -625,7 +625,7 @@ int gemm_configs(GemmKind kind, const GemmConfig** out) {
         case KIND_BF16: *out = kBF16Cfgs; return (int)(sizeof(kBF16Cfgs) / sizeof(kBF16Cfgs[0]));
         case KIND_F32: *out = kF32Cfgs; return (int)(sizeof(kF32Cfgs) / sizeof(kF32Cfgs[0]));
         case KIND_I8: *out = kI8Cfgs; return (int)(sizeof(kI8Cfgs) / sizeof(kI8Cfgs[0]));
-        // the hi/lo kind runs the bf16 kernels over twice the k-tiles: the same tiles
+        // the hi/lo kind uses the bf16 kind's tiles (see gemm_kernel for how it runs on them)
         case KIND_BF16X2: *out = kBF16Cfgs; return (int)(sizeof(kBF16Cfgs) / sizeof(kBF16Cfgs[0]));
     }
     return 0;
