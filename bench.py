@@ -206,7 +206,8 @@ class Dit:
     def zero_operand_rate(self):
         """The same kernels, shapes and launch order on all-zero A and weights. The schedule, the data movement
         and the instruction stream are identical; only the operand bits differ, so the gap to the random-data
-        rate is what the MFMA arrays' data-dependent power costs (the clock drops under the power limit)."""
+        rate is what the operand values cost through the MFMA arrays' power draw (the clock drops under the
+        power limit). Time bound by operand traffic (MLP-down in this order) is the same for both."""
         L, s = self.L, self.sess
         a16 = {k: s.empty(L.DT_BF16, (self.M, k)) for k in (3072, 12288)}
         for t in a16.values():
