@@ -669,3 +669,64 @@ def test_hilo_random_shapes_and_row_invariance(sess, seed):
     small = run_gemm(sess, da, w, m_small, **kw)
     assert np.array_equal(small, got[:m_small]), f"rows differ between M={m_small} and M={m}"
     w.free(), da.free(), db.free()
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16", "i8"])
+@pytest.mark.parametrize("seed", range(8))
+def test_random_shapes_all_kinds(sess, kind, seed):
+    """Random shapes across every GEMM kind and the tile heuristic's whole range (M from 1 to ~1400, N and K
+    ragged): f32 weights held to the reference's relative 1e-5·sqrt(K) (kernels/gemm/gemm_test.go:34), bf16
+    math to the north-star bound, int8 MatMulInteger + dequant bit-exact; and, except where the decode GEMV
+    takes the small call (bf16, M <= 16), rows shared by a small and a large call are bit-identical
+    (kernels/gemm/minvariance_test.go:21)."""
+    rng = np.random.default_rng(7100 + 97 * seed + len(kind))
+    m = int(rng.integers(1, 1400))
+    n = int(rng.integers(1, 3000))
+    k = int(rng.integers(1, 2500))
+    m_small = int(rng.integers(1, min(m, 200) + 1))
+    announce(f"random {kind} seed={seed} m={m} m_small={m_small} n={n} k={k}")
+    if kind == "i8":
+        a = rng.integers(0, 256, (m, k)).astype(np.uint8)
+        b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+        za = int(rng.integers(0, 256))
+        sc = rng.uniform(0.001, 0.01, n).astype(np.float32)
+        w = sess.upload_weight(b, trans=False, pack_dtype=L.DT_I8)
+        da, ds = sess.to_device(a, L.DT_U8), sess.to_device(sc)
+
+        def run(mm):
+            yi, yf = sess.empty(L.DT_I32, (mm, n)), sess.empty(L.DT_F32, (mm, n))
+            sess.matmul_integer(da, w, mm, za, y_i32=yi, scale=ds, y_f32=yf)
+            return yi.numpy(), yf.numpy()
+
+        yi, yf = run(m)
+        want = oracle.matmul_integer(a, b, za)
+        assert np.array_equal(yi, want), "int8 products"
+        assert np.array_equal(yf, oracle.dequantize_linear(want, sc, inner=1)), "int8 dequant"
+        w.free(), da.free(), ds.free()
+        return
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    db = sess.to_device(bias)
+    kw = dict(beta=1.0, c=db, c_mode=L.C_ROW, act=L.ACT_RELU)
+    if kind == "f32":
+        bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+        w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_F32)
+        wide, okw, ain = bt, {}, a
+    else:
+        bt = bf16_weights(rng, (n, k))
+        w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+        wide, okw = oracle.bf16_to_f32(bt), {"b_dtype": oracle.BF16}
+        kw["math"] = L.MATH_BF16
+        ain = oracle.bf16_to_f32(oracle.f32_to_bf16(a))
+    da = sess.to_device(a)
+    got = run_gemm(sess, da, w, m, **kw)
+    rows = np.unique(np.concatenate([np.arange(min(m, 24)), rng.integers(0, m, 40)]))
+    want = oracle.gemm(np.ascontiguousarray(ain[rows]), bt, trans_b=True, beta=1.0, c=bias, c_mode=L.C_ROW,
+                       act_code=L.ACT_RELU, **okw)
+    assert_close(got[rows], want, nstar_tol(k, a, wide), f"{kind} {m}x{n}x{k}")
+    if kind == "f32":
+        rel = np.max(np.abs(got[rows] - want) / np.maximum(np.abs(want), 1.0))
+        assert rel <= 1e-5 * math.sqrt(k), f"f32 relative error {rel:.3e}"
+    if kind == "f32" or m_small > 16:
+        assert np.array_equal(run_gemm(sess, da, w, m_small, **kw), got[:m_small]), f"rows M={m_small} vs M={m}"
+    w.free(), da.free(), db.free()
