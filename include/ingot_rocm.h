@@ -187,7 +187,12 @@ int ingot_rocm_weight_info(const ingot_rocm_weight* w, int64_t* n, int64_t* k, i
  * Routing of bf16 weights with f32 A (no transA, batch 1): M <= 4 runs the
  * decode GEMV of ingot_rocm_gemv_bf16, and so does M = 5..16 when N < 4096;
  * M = 5..16 with N >= 4096 runs the GEMM (four-stage 32x32 tiles), which is
- * faster there. ingot_rocm_gemv_bf16 always runs the GEMV (M <= 16). */
+ * faster there. ingot_rocm_gemv_bf16 always runs the GEMV (M <= 16).
+ * A row of Y does not depend on M (kernels/gemm/minvariance_test.go:21): every
+ * GEMM tile of one weight/math kind sums K in the same order, so rows are
+ * bit-identical across M for f32 weights, and for bf16 weights at every M the
+ * GEMM serves (above); the GEMV sums in its own order, as the reference's M = 1
+ * GEMV does. int8 results are exact. */
 typedef struct ingot_rocm_gemm_args {
     int64_t M, N, K;
     const void* d_a;
