@@ -55,7 +55,8 @@ inline float bf16f(uint16_t h) {
 // Each helper has its own mailbox (a generation number): the caller fills in the region, then bumps the
 // mailboxes of the helpers it enlists and waits until each of them has finished, so a helper never reads a
 // region that is not its own. Helpers spin on their mailbox for about 50 µs, then sleep on a condition
-// variable, so back-to-back regions start without a thread wake-up. One region runs at a time.
+// variable, so back-to-back regions start without a thread wake-up. One region runs at a time, and a
+// region's task must not start another (the pool would wait on itself).
 class Pool {
 public:
     static constexpr int kMaxHelpers = 255;
