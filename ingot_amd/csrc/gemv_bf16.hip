@@ -1,6 +1,7 @@
 // Decode GEMV for gfx950: y[m,n] = epilogue(Σ_k x[m,k]·W[n,k]) for M <= 16
-// rows of f32 activations against a packed bf16 weight [Np][Kp]. Two kernels:
-// M <= 4 streams weight rows whole with VALU FMAs (gemv_rows_kernel, below);
+// rows of f32 activations against a packed bf16 weight [Np][Kp]. M <= 4
+// streams weight rows with VALU FMAs — straight into registers at M = 1
+// (gemv_rows_kernel, below), through LDS at M = 2..4 (gemv_dma_kernel) — and
 // M = 5..16 runs the MFMA kernel described here.
 //
 // HBM-bound: the weight is streamed exactly once with 16-byte loads, and all
@@ -264,6 +265,171 @@ hipError_t launch_rows(const A& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+// ---- M <= 4: weight rows streamed through LDS by DMA ----
+// The rows kernel holds every in-flight weight chunk, and the activations that
+// go with it, in registers, which at M = 3..4 leaves one 512-k chunk per wave
+// in flight. Here the weight moves global → LDS by DMA (buffer_load_dwordx4
+// ... lds, no registers held while a load is in flight), D units ahead per
+// wave, a unit being R weight rows × 512 k; x is staged in LDS once per
+// workgroup. Each lane reads back exactly the 16 bytes it fetched, and its
+// activations from the staged copy, so after the start no wave waits for
+// another: it waits on its own DMA (vmcnt; loads complete in issue order).
+// Persistent grid: wave g of G takes row groups g, g + G, ...; per row group
+// the FMAs run in the rows kernel's order (chunk by chunk, the same sequence)
+// and the same butterfly adds the lane partials, so y is bit-identical to it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+#define LDS_AS(ptr) ((__attribute__((address_space(3))) void*)(ptr))
+
+// s_waitcnt vmcnt(V) expcnt(7) lgkmcnt(15) / vmcnt(63) expcnt(7) lgkmcnt(0)
+template <int V>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(V >= 0 && V < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | 0x70 | 0xF00);
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | 0x70); }
+
+template <int R, int MM, int NW, int D, int XC>
+__global__ __launch_bounds__(64 * NW) void gemv_dma_kernel(GemvArgs p) {
+    constexpr int XBYTES = MM * XC * 2048;  // x: [MM][XC][2] blocks, lane l's 16 bytes at 16·l
+    constexpr int UBYTES = R * 1024;         // one unit: R rows × 512 k of bf16
+    static_assert(XBYTES + NW * D * UBYTES <= 160 * 1024, "LDS must fit in 160 KiB");
+    static_assert(D * R < 64, "outstanding DMA must fit the 6-bit vmcnt");
+    __shared__ __attribute__((aligned(1024))) char lds[XBYTES + NW * D * UBYTES];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int chunks = (int)((p.kp + 511) / 512);  // <= XC (the host checks)
+    const int gw = blockIdx.x * NW + wave;
+    const int GW = gridDim.x * NW;
+    const int T = (p.N + R - 1) / R;  // row groups
+    const int units = gw < T ? ((T - 1 - gw) / GW + 1) * chunks : 0;
+
+    // x → LDS: block (m, c, h) holds x[m][512c + 8l + 4h .. +3] in lane l's 16 bytes
+    // (zero for m >= M and past K: the host requires K % 4 == 0)
+    const __amdgpu_buffer_rsrc_t rsx = make_rsrc(p.x, (uint32_t)(((int64_t)(p.M - 1) * p.ldx + p.K) * 4));
+    for (int b = wave; b < MM * chunks * 2; b += NW) {
+        const int h = b & 1, c = (b >> 1) % chunks, m = (b >> 1) / chunks;
+        const int k = c * 512 + lane * 8 + h * 4;
+        const uint32_t off = m < p.M && k + 4 <= p.K ? (uint32_t)(((int64_t)m * p.ldx + k) * 4) : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, LDS_AS(lds + ((m * XC + c) * 2 + h) * 1024), 16, off, 0, 0, 0);
+    }
+
+    // weight units → this wave's ring of D slots; past the last unit (or past
+    // kp, or row >= N) the offset is out of range and the slot fills with zeros,
+    // so every unit issues exactly R loads
+    const __amdgpu_buffer_rsrc_t rsw = make_rsrc(p.w, (uint32_t)((int64_t)p.N * p.ldw * 2));
+    char* ring = lds + XBYTES + wave * (D * UBYTES);
+    int iu = 0, it = 0, ic = 0, islot = 0;  // next unit to issue: index, row group (this wave's), chunk, slot
+    auto issue = [&]() {
+        const int k = ic * 512 + lane * 8;
+        const bool live = iu < units && k < p.kp;
+        const int row0 = (gw + it * GW) * R;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t off =
+                live && row0 + r < p.N ? (uint32_t)(((int64_t)(row0 + r) * p.ldw + k) * 2) : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, LDS_AS(ring + islot * UBYTES + r * 1024), 16, off, 0, 0, 0);
+        }
+        ++iu;
+        if (++ic == chunks) {
+            ic = 0;
+            ++it;
+        }
+        islot = islot + 1 == D ? 0 : islot + 1;
+    };
+    static_assert(D >= 2, "one slot is refilled while the others are in flight");
+#pragma unroll
+    for (int s = 0; s < D - 1; ++s) issue();
+    wait_vm<(D - 1) * R>();  // this wave's x blocks (issued before its units) have landed
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave's x blocks have landed
+    asm volatile("" ::: "memory");
+
+    float acc[R][MM];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) acc[r][m] = 0.f;
+    int ct = 0, cc = 0, cslot = 0;  // unit consumed next: row group, chunk, slot
+    for (int u = 0; u < units; ++u) {
+        // unit u has landed (D - 1 units in flight, in issue order), and the
+        // previous unit's LDS reads have returned: its slot is refilled below
+        wait_vm<(D - 2) * R>();
+        wait_lgkm0();
+        asm volatile("" ::: "memory");
+        const char* slot = ring + cslot * UBYTES;
+        i32x4_t w[R];
+        f32x4_t xa[MM][2];
+#pragma unroll
+        for (int r = 0; r < R; ++r) w[r] = *(const i32x4_t*)(slot + r * 1024 + lane * 16);
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) xa[m][h] = *(const f32x4_t*)(lds + ((m * XC + cc) * 2 + h) * 1024 + lane * 16);
+        issue();  // unit u + D - 1 → the slot of unit u - 1
+        float xv[MM][8];
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[m][e] = xa[m][e >> 2][e & 3];
+        if (!p.split) {
+#pragma unroll
+            for (int m = 0; m < MM; ++m)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[m][e] = bf16_to_f32(f32_to_bf16(xv[m][e]));
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t* wb = (const uint32_t*)&w[r];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = __uint_as_float(wb[e] << 16);
+                const float hi = __uint_as_float(wb[e] & 0xFFFF0000u);
+#pragma unroll
+                for (int m = 0; m < MM; ++m) {
+                    acc[r][m] = fmaf(xv[m][2 * e], lo, acc[r][m]);
+                    acc[r][m] = fmaf(xv[m][2 * e + 1], hi, acc[r][m]);
+                }
+            }
+        }
+        if (++cc == chunks) {
+            reduce_store<R, MM>(acc, lane, (gw + ct * GW) * R, p);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < MM; ++m) acc[r][m] = 0.f;
+            cc = 0;
+            ++ct;
+        }
+        cslot = cslot + 1 == D ? 0 : cslot + 1;
+    }
+    wait_vm<0>();  // the tail's zero-fill loads land before the workgroup's LDS is released
+}
+
+// What gemv_dma_kernel assumes: whole 16-byte x pieces (K % 4 == 0), rows of
+// at most 12 chunks of 512 k (x staged whole in LDS), 32-bit buffer offsets,
+// and the device's CU count for the persistent grid.
+bool dma_ok(const GemvArgs& a) {
+    return a.K % 4 == 0 && a.cus > 0 && (a.kp + 511) / 512 <= 12 && (int64_t)a.N * a.ldw * 2 < (1ll << 31) &&
+           ((int64_t)(a.M - 1) * a.ldx + a.K) * 4 < (1ll << 31);
+}
+
+template <int R, int MM, int NW, int D>
+hipError_t launch_dma(const GemvArgs& a, hipStream_t st) {
+    if (a.M > MM || !dma_ok(a)) return hipErrorInvalidValue;
+    const int64_t chunks = (a.kp + 511) / 512;
+    const int T = (a.N + R - 1) / R;
+    auto go = [&](auto kern, int bytes) {
+        const int occ = std::max(1, 160 * 1024 / bytes);
+        const int grid = std::min((T + NW - 1) / NW, a.cus * occ);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), 0, st, a);
+        return hipGetLastError();
+    };
+    if (chunks <= 4) return go(gemv_dma_kernel<R, MM, NW, D, 4>, MM * 4 * 2048 + NW * D * R * 1024);
+    return go(gemv_dma_kernel<R, MM, NW, D, 12>, MM * 12 * 2048 + NW * D * R * 1024);
+}
+
 // GemvPlainArgs seen through the members gemv_rows_kernel reads: the fixed
 // parts of the plain case are compile-time constants, and its epilogue is the
 // identity with an f32 store.
@@ -320,6 +486,13 @@ hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st) {
         // 5632-long rows of the decode down projection took 6.1 µs instead of 6.5.
         const int64_t chunks = (a.kp + 511) / 512;
         if (a.M == 1) return chunks > 4 && chunks <= 12 ? launch_rows<1, 1, 4, 12>(a, st) : launch_rows<1, 1>(a, st);
+        // M = 2..4: the weight streamed through LDS (gemv_dma_kernel). On MI355X
+        // the decode step of the four GEMVs (QKV, O, gate+up, down) took
+        // 33.8–35.6 instead of 43.1–43.4 µs at M = 4, 33.0–34.1 instead of 44.0
+        // at M = 3 and 30.8–32.0 instead of 34.8–35.5 at M = 2 (at M = 1 it was
+        // slower: 28.7 against 25.5–25.9 µs). The row kernels below remain for
+        // shapes outside its preconditions.
+        if (a.M <= 4 && dma_ok(a)) return a.M == 2 ? launch_dma<1, 2, 8, 4>(a, st) : launch_dma<1, 4, 8, 4>(a, st);
         if (a.M == 2) return launch_rows<1, 2>(a, st);
         // M = 3..4: one chunk in flight per step keeps these kernels at 46–54
         // VGPRs (8+ waves per SIMD: the 5632 waves of N = 11264 fit in one
@@ -348,6 +521,10 @@ hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st) {
             case 20: return launch_rows<1, 1, 4, 12>(a, st);
             case 21: return launch_rows<2, 4, 1, 1>(a, st);
             case 22: return launch_rows<1, 4, 4, 1>(a, st);
+            case 23: return launch_dma<1, 4, 8, 4>(a, st);
+            case 24: return launch_dma<1, 2, 8, 4>(a, st);
+            case 25: return launch_dma<1, 1, 8, 4>(a, st);
+            case 26: return launch_dma<2, 4, 8, 3>(a, st);
         }
         return hipErrorInvalidValue;
     }

@@ -81,6 +81,7 @@ struct GemvArgs {
     Epi epi;
     void* y;  // f32 or bf16 per epi.y_bf16
     int64_t ldy;
+    int cus;  // compute units of the device (sizes persistent grids; not read by kernels)
 };
 // cfg selects (waves per workgroup, 16-byte chunks per lane per round).
 hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st);

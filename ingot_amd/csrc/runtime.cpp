@@ -484,6 +484,7 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const 
     g.epi = make_epi(a);
     g.y = a->d_y;
     g.ldy = a->ldy;
+    g.cus = s->num_cus;
     if (a->M > 4) {
         // the MFMA kernel reads x as fragment-ordered bf16 planes (hi, lo)
         void* ws;

@@ -255,8 +255,10 @@ def test_gemv_i8g_declines_prefill(sess):
 
 
 @pytest.mark.parametrize("m", [1, 2, 4, 7, 16])
-@pytest.mark.parametrize("n,k", [(64, 256), (200, 300), (2048, 2048), (1000, 5632)])
+@pytest.mark.parametrize("n,k", [(64, 256), (200, 300), (2048, 2048), (1000, 5632), (96, 1001), (64, 7000)])
 def test_gemv_bf16_decode(sess, m, n, k):
+    """K = 1001 (not a multiple of 4) and K = 7000 (longer than the LDS-staged rows) take the row kernels at
+    M = 2..4; the other shapes the LDS-DMA kernel."""
     announce(f"gemv m={m} n={n} k={k}")
     rng = np.random.default_rng(m * 1000 + n + k)
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
@@ -341,13 +343,13 @@ def test_gemm_forced_tile_configs(env_session, kind, cfg, m, n, k):
 
 
 @pytest.mark.parametrize("cfg", ["10", "11", "12", "13", "14", "15", "16", "17", "18", "19", "20", "21", "22",
-                                 "1", "2", "3", "4", "5", "6", "7"])
+                                 "23", "24", "25", "26", "1", "2", "3", "4", "5", "6", "7"])
 @pytest.mark.parametrize("m", [1, 2, 4, 9, 16])
 def test_gemv_forced_configs(env_session, cfg, m):
     """Every GEMV launch configuration (INGOT_GEMV_CFG) that applies to M, strided x, both math modes."""
     rows_cfg = int(cfg) >= 10
     mm = {"10": 1, "11": 1, "12": 1, "13": 4, "14": 4, "15": 2, "16": 4, "17": 4, "18": 4, "19": 2,
-          "20": 1, "21": 4, "22": 4}.get(cfg, 16)
+          "20": 1, "21": 4, "22": 4, "23": 4, "24": 2, "25": 1, "26": 4}.get(cfg, 16)
     if (m > 4) == rows_cfg or m > mm:
         pytest.skip("configuration does not cover this M")
     announce(f"gemv cfg={cfg} m={m}")
