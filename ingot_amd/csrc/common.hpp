@@ -28,6 +28,37 @@ __host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return f;
 }
 
+// The 32 bits lane ^ off holds (off = 32, 16, ..., 1: a butterfly partner),
+// moved by VALU lane permutes instead of the LDS crossbar (ds_bpermute):
+// off = 32 and 16 by the permlane swaps, which trade the upper half (of the
+// wave, or of each pair of 16-lane rows) of one copy of u with the lower half
+// of another, so lane l finds its partner in the copy whose half it is not in;
+// 8 by a rotation of each row by 8 lanes; 4 by two row shifts, each written to
+// the 4-lane banks that take from that direction; 2 and 1 by quad
+// permutations. All 64 lanes must be active.
+__device__ __forceinline__ int xor_partner_bits(int u, int off, int lane) {
+    switch (off) {
+        case 32: {
+            const auto s = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+            return (int)((lane & 32) ? s[0] : s[1]);
+        }
+        case 16: {
+            const auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+            return (int)((lane & 16) ? s[0] : s[1]);
+        }
+        case 8: return __builtin_amdgcn_update_dpp(0, u, 0x128, 0xF, 0xF, false);  // row_ror:8
+        case 4: {
+            const int t = __builtin_amdgcn_update_dpp(0, u, 0x104, 0xF, 0x5, false);  // row_shl:4, banks 0, 2
+            return __builtin_amdgcn_update_dpp(t, u, 0x114, 0xF, 0xA, false);         // row_shr:4, banks 1, 3
+        }
+        case 2: return __builtin_amdgcn_update_dpp(0, u, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+        default: return __builtin_amdgcn_update_dpp(0, u, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+    }
+}
+__device__ __forceinline__ float xor_partner(float x, int off, int lane) {
+    return __int_as_float(xor_partner_bits(__float_as_int(x), off, lane));
+}
+
 // f32 x as two bf16 terms, hi + lo = x to within 2⁻¹⁷|x|, so that hi·w + lo·w
 // over a bf16 w keeps f32-activation accuracy: hi = bf16(x) (RNE), lo =
 // bf16(x − hi). Two cases keep the products IEEE-faithful: a finite x whose

@@ -147,34 +147,6 @@ __global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemvArgs p) {
 // is bit-identical to one, with V − 1 + log2(64 / V) exchanges instead of 6·V.
 // Sum j (= r·MM + m) ends in the lanes whose bits 5, 4, ... (one per halving)
 // spell j; the one with the other bits clear stores it.
-// The value lane ^ off holds, moved by VALU lane permutes instead of the LDS
-// crossbar (ds_bpermute): off = 32 and 16 by the permlane swaps, which trade
-// the upper half (of the wave, or of each pair of 16-lane rows) of one copy of
-// x with the lower half of another, so lane l finds its partner in the copy
-// whose half it is not in; 8 by a rotation of each row by 8 lanes; 4 by two
-// row shifts, each written to the 4-lane banks that take from that direction;
-// 2 and 1 by quad permutations. All 64 lanes must be active.
-__device__ __forceinline__ float xor_partner(float x, int off, int lane) {
-    const int u = __float_as_int(x);
-    switch (off) {
-        case 32: {
-            const auto s = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-            return __int_as_float((lane & 32) ? s[0] : s[1]);
-        }
-        case 16: {
-            const auto s = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-            return __int_as_float((lane & 16) ? s[0] : s[1]);
-        }
-        case 8: return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x128, 0xF, 0xF, false));  // row_ror:8
-        case 4: {
-            const int t = __builtin_amdgcn_update_dpp(0, u, 0x104, 0xF, 0x5, false);      // row_shl:4, banks 0, 2
-            return __int_as_float(__builtin_amdgcn_update_dpp(t, u, 0x114, 0xF, 0xA, false));  // row_shr:4, banks 1, 3
-        }
-        case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
-        default: return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
-    }
-}
-
 template <int R, int MM, typename A>
 __device__ __forceinline__ void reduce_store(float (&acc)[R][MM], int lane, int row0, const A& p) {
     constexpr int V = R * MM;

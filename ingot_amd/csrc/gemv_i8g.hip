@@ -24,9 +24,9 @@ namespace {
 constexpr int G = 64;             // I8Group
 constexpr float X16_MAX = 16256;  // 127·128
 
-__device__ __forceinline__ float wave_max(float v) {
+__device__ __forceinline__ float wave_max(float v, int lane) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, xor_partner(v, off, lane));
     return v;
 }
 
@@ -46,7 +46,7 @@ __global__ void quantize_w_kernel(const void* src, int src_dt, int64_t ld, int t
     const int64_t kk = g * G + lane;
     const bool in = j < n && kk < k;
     const float v = in ? load_w(src, src_dt, trans ? j * ld + kk : kk * ld + j) : 0.f;
-    const float s = wave_max(fabsf(v)) / 127.f;
+    const float s = wave_max(fabsf(v), lane) / 127.f;
     int qi = 0;
     if (s != 0.f) qi = (int)fminf(127.f, fmaxf(-127.f, rintf(v / s)));
     q[j * ldk + kk] = (int8_t)qi;
@@ -64,7 +64,7 @@ __global__ void quantize_x_kernel(const float* x, int64_t ldx, int M, int64_t K,
     const int64_t m = wid / gk, g = wid - m * gk;
     const int64_t kk = g * G + lane;
     const float v = kk < K ? x[m * ldx + kk] : 0.f;
-    const float s = wave_max(fabsf(v)) / X16_MAX;
+    const float s = wave_max(fabsf(v), lane) / X16_MAX;
     int h = 0, l = 0;
     if (s != 0.f) {
         const float inv = 1.f / s;
@@ -139,8 +139,8 @@ __global__ __launch_bounds__(256) void gemv_i8g_kernel(I8gArgs p) {
                         pl = __builtin_amdgcn_sdot4(w[c][r][e], l[c][m][e], pl, false);
                     }
                     int part = 128 * ph + pl;
-                    part += __shfl_xor(part, 1);
-                    part += __shfl_xor(part, 2);
+                    part += xor_partner_bits(part, 1, lane);
+                    part += xor_partner_bits(part, 2, lane);
                     if (store && (lane & 3) == 0) {
                         const float st = sx[c][m] * sw[c][r];
                         t[(r * MM + m) * gk + g] = st * (float)part;
