@@ -1,8 +1,9 @@
 // Decode GEMV for gfx950: y[m,n] = epilogue(Σ_k x[m,k]·W[n,k]) for M <= 16
-// rows of f32 activations against a packed bf16 weight [Np][Kp]. M <= 4
+// rows of f32 activations against a packed bf16 weight [Np][Kp]. M <= 8
 // streams weight rows with VALU FMAs — straight into registers at M = 1
-// (gemv_rows_kernel, below), through LDS at M = 2..4 (gemv_dma_kernel) — and
-// M = 5..16 runs the MFMA kernel described here.
+// (gemv_rows_kernel, below), through LDS at M = 2..4 and at M = 5..8 with
+// K <= 2048 (gemv_dma_kernel) — and the other M <= 16 products run the MFMA
+// kernel described here.
 //
 // HBM-bound: the weight is streamed exactly once with 16-byte loads, and all
 // of a wave's loads for a round are issued before any MFMA waits on them.
@@ -411,8 +412,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_dma_kernel(GemvArgs p) {
 // at most 12 chunks of 512 k (x staged whole in LDS), 32-bit buffer offsets,
 // and the device's CU count for the persistent grid.
 bool dma_ok(const GemvArgs& a) {
-    return a.K % 4 == 0 && a.cus > 0 && (a.kp + 511) / 512 <= 12 && (int64_t)a.N * a.ldw * 2 < (1ll << 31) &&
-           ((int64_t)(a.M - 1) * a.ldx + a.K) * 4 < (1ll << 31);
+    return gemv_dma_fits(a.M, a.K, a.kp, a.N, a.ldw, a.ldx) && a.cus > 0;
 }
 
 template <int R, int MM, int NW, int D>
@@ -427,7 +427,10 @@ hipError_t launch_dma(const GemvArgs& a, hipStream_t st) {
         return hipGetLastError();
     };
     if (chunks <= 4) return go(gemv_dma_kernel<R, MM, NW, D, 4>, MM * 4 * 2048 + NW * D * R * 1024);
-    return go(gemv_dma_kernel<R, MM, NW, D, 12>, MM * 12 * 2048 + NW * D * R * 1024);
+    // rows of 5..12 chunks: x for 8 activation rows would not fit (dma_ok sends M > 4 here only up to 4 chunks)
+    if constexpr (MM * 12 * 2048 + NW * D * R * 1024 <= 160 * 1024)
+        return go(gemv_dma_kernel<R, MM, NW, D, 12>, MM * 12 * 2048 + NW * D * R * 1024);
+    return hipErrorInvalidValue;
 }
 
 // GemvPlainArgs seen through the members gemv_rows_kernel reads: the fixed
@@ -476,8 +479,28 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+bool gemv_cfg_is_dma(int cfg) { return cfg >= 23 && cfg <= 30; }
+
+bool gemv_dma_fits(int M, int64_t K, int64_t kp, int64_t N, int64_t ldw, int64_t ldx) {
+    const int64_t chunks = (kp + 511) / 512;
+    return M >= 1 && M <= 8 && K % 4 == 0 && chunks <= (M <= 4 ? 12 : 4) && N * ldw * 2 < (1ll << 31) &&
+           ((int64_t)(M - 1) * ldx + K) * 4 < (1ll << 31);
+}
+
 hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st) {
     if (a.kp % KR != 0 || a.M < 1 || a.M > 16) return hipErrorInvalidValue;
+    // M = 5..8 with x for 8 rows staged whole (K <= 2048): no x pre-pass launch.
+    // On MI355X at K = 2048, M = 8: N = 2048 6.3 instead of 9.8 µs (pre-pass
+    // + MFMA kernel); N = 6144 12.2, N = 11264 20.0 µs (the runtime sends
+    // N >= 4096 to the GEMM, 14.8 and 13.7 µs there, which keeps those rows
+    // bit-identical to larger M).
+    if (cfg == 0 && a.M >= 5 && a.M <= 8 && dma_ok(a)) return launch_dma<1, 8, 8, 4>(a, st);
+    switch (cfg) {  // M <= 8, x read in place (no pre-pass)
+        case 27: return launch_dma<1, 8, 8, 4>(a, st);
+        case 28: return launch_dma<1, 8, 16, 3>(a, st);
+        case 29: return launch_dma<1, 8, 16, 2>(a, st);
+        case 30: return launch_dma<1, 8, 12, 3>(a, st);
+    }
     if (a.M > 4 && !a.xb) return hipErrorInvalidValue;
     if (cfg == 0) {  // default: rows kernel for M <= 4, MFMA kernel above (measured on MI355X)
         // M = 1 with rows of 5..12 chunks of 512 k: a whole row in flight per

@@ -85,6 +85,12 @@ struct GemvArgs {
 };
 // cfg selects (waves per workgroup, 16-byte chunks per lane per round).
 hipError_t launch_gemv_bf16(const GemvArgs& a, int cfg, hipStream_t st);
+// Whether the LDS-DMA GEMV can take these operands (x staged whole in LDS:
+// M <= 4 with rows up to 6144 k, M = 5..8 up to 2048 k; K % 4 == 0; 32-bit
+// buffer offsets). At cfg 0 it serves M = 2..8, without the x pre-pass.
+bool gemv_dma_fits(int M, int64_t K, int64_t kp, int64_t N, int64_t ldw, int64_t ldx);
+// Forced configurations (INGOT_GEMV_CFG) of the LDS-DMA GEMV.
+bool gemv_cfg_is_dma(int cfg);
 // The common decode case in a small argument block (the host cost of a launch
 // grows with the argument size; these 40 bytes launch as 48, against 152 for
 // GemvArgs): M = 1, f32 x 16-byte aligned, f32-class math (split), y = x·Wᵀ

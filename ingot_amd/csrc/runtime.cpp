@@ -485,7 +485,9 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const 
     g.y = a->d_y;
     g.ldy = a->ldy;
     g.cus = s->num_cus;
-    if (a->M > 4) {
+    const int cfg = s->force_gemv_cfg;
+    const bool dma = (cfg == 0 || gemv_cfg_is_dma(cfg)) && gemv_dma_fits(g.M, g.K, g.kp, g.N, g.ldw, g.ldx);
+    if (a->M > 4 && !dma) {
         // the MFMA kernel reads x as fragment-ordered bf16 planes (hi, lo)
         void* ws;
         int rc = call_ws(s, noalloc, (size_t)((g.split ? 2 : 1) * 16 * w->kp * 2), &ws);
@@ -496,7 +498,6 @@ static int run_gemv(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const 
         g.xb = (const uint16_t*)ws;
         g.xb_plane = 16 * w->kp;
     }
-    const int cfg = s->force_gemv_cfg;
     hipError_t e = cfg == 0 && gemv_plain_ok(g) ? launch_gemv_plain(g, s->stream) : launch_gemv_bf16(g, cfg, s->stream);
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return INGOT_OK;

@@ -343,14 +343,14 @@ def test_gemm_forced_tile_configs(env_session, kind, cfg, m, n, k):
 
 
 @pytest.mark.parametrize("cfg", ["10", "11", "12", "13", "14", "15", "16", "17", "18", "19", "20", "21", "22",
-                                 "23", "24", "25", "26", "1", "2", "3", "4", "5", "6", "7"])
-@pytest.mark.parametrize("m", [1, 2, 4, 9, 16])
+                                 "23", "24", "25", "26", "27", "28", "29", "30", "1", "2", "3", "4", "5", "6", "7"])
+@pytest.mark.parametrize("m", [1, 2, 4, 6, 9, 16])
 def test_gemv_forced_configs(env_session, cfg, m):
     """Every GEMV launch configuration (INGOT_GEMV_CFG) that applies to M, strided x, both math modes."""
-    rows_cfg = int(cfg) >= 10
+    rows_cfg = 10 <= int(cfg) <= 26  # VALU kernels for M <= 4
     mm = {"10": 1, "11": 1, "12": 1, "13": 4, "14": 4, "15": 2, "16": 4, "17": 4, "18": 4, "19": 2,
-          "20": 1, "21": 4, "22": 4, "23": 4, "24": 2, "25": 1, "26": 4}.get(cfg, 16)
-    if (m > 4) == rows_cfg or m > mm:
+          "20": 1, "21": 4, "22": 4, "23": 4, "24": 2, "25": 1, "26": 4, "27": 8, "28": 8, "29": 8, "30": 8}.get(cfg, 16)
+    if (rows_cfg and m > 4) or (int(cfg) < 10 and m <= 4) or m > mm:
         pytest.skip("configuration does not cover this M")
     announce(f"gemv cfg={cfg} m={m}")
     sess = env_session(INGOT_GEMV_CFG=cfg)
