@@ -28,6 +28,15 @@ __host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return f;
 }
 
+// A raw buffer resource over [base, base + bytes): loads at offsets past
+// `bytes` return zero (and LDS-DMA loads write zeros), so kernels bound their
+// reads by the resource instead of by branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// An LDS address as the LDS-DMA builtins take it.
+#define LDS_AS(ptr) ((__attribute__((address_space(3))) void*)(ptr))
+
 // The 32 bits lane ^ off holds (off = 32, 16, ..., 1: a butterfly partner),
 // moved by VALU lane permutes instead of the LDS crossbar (ds_bpermute):
 // off = 32 and 16 by the permlane swaps, which trade the upper half (of the

@@ -74,12 +74,6 @@ __device__ __forceinline__ void mma16<KIND_I8>(i32x4_t& acc, const i32x4_t& x, c
     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x, y, acc, 0, 0, 0);
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-#define LDS_AS(ptr) ((__attribute__((address_space(3))) void*)(ptr))
-
 // The workgroup barrier does not wait for LDS-DMA loads (they count as
 // vector-memory loads, not LDS stores), so before it every wave waits until at
 // most `groups` of its k-tile DMA groups (G instructions each) are in flight,

@@ -278,11 +278,6 @@ hipError_t launch_rows(const A& a, hipStream_t st) {
 // Persistent grid: wave g of G takes row groups g, g + G, ...; per row group
 // the FMAs run in the rows kernel's order (chunk by chunk, the same sequence)
 // and the same butterfly adds the lane partials, so y is bit-identical to it.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-#define LDS_AS(ptr) ((__attribute__((address_space(3))) void*)(ptr))
-
 // s_waitcnt vmcnt(V) expcnt(7) lgkmcnt(15) / vmcnt(63) expcnt(7) lgkmcnt(0)
 template <int V>
 __device__ __forceinline__ void wait_vm() {
