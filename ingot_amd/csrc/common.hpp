@@ -142,8 +142,12 @@ __device__ __forceinline__ float apply_act(float x, int act, float a, float b) {
         case INGOT_ACT_RELU: return fmaxf(x, 0.f);
         case INGOT_ACT_GELU_ERF: return 0.5f * x * (1.f + erf_as(x * 0.70710678118654752f));
         case INGOT_ACT_GELU_TANH: {
-            float u = x + 0.044715f * x * x * x;
-            return 0.5f * x * (1.f + tanhf(0.7978845608028654f * u));
+            // tanh(v) = 1 − 2/(e^{2v} + 1) with the hardware exponential and
+            // reciprocal: a few ulp of 1 absolute, which is all 1 + tanh needs,
+            // and ±1 (not NaN) where e^{2v} overflows or vanishes
+            const float v = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+            const float t = 1.f - 2.f * __builtin_amdgcn_rcpf(__expf(2.f * v) + 1.f);
+            return 0.5f * x * (1.f + t);
         }
         case INGOT_ACT_SIGMOID: return 1.f / (1.f + exp_clamped(-x));
         case INGOT_ACT_SILU: return x / (1.f + exp_clamped(-x));
