@@ -111,12 +111,17 @@ __device__ __forceinline__ void store_y(void* y, int64_t i, float v, const Epi& 
         ((float*)y)[i] = v;
 }
 
-// exp with the argument clamp of expScalar (kernels/vek/scalar.go:7-13).
-__device__ __forceinline__ float exp_clamped(float x) {
-    return __expf(fminf(fmaxf(x, -87.33654f), 88.37626f));
+// The clamps compare, as Go's min and max do: a NaN passes through (fminf and
+// fmaxf would return the bound instead).
+__device__ __forceinline__ float clamp_to(float x, float lo, float hi) {
+    x = x < lo ? lo : x;
+    return x > hi ? hi : x;
 }
 
-__device__ __forceinline__ float clamp01(float x) { return fminf(fmaxf(x, 0.f), 1.f); }
+// exp with the argument clamp of expScalar (kernels/vek/scalar.go:7-13).
+__device__ __forceinline__ float exp_clamped(float x) { return __expf(clamp_to(x, -87.33654f, 88.37626f)); }
+
+__device__ __forceinline__ float clamp01(float x) { return clamp_to(x, 0.f, 1.f); }
 
 // erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7), the approximation
 // the reference's amd64 GELU kernel evaluates (kernels/vek/genamd64/main.go:62-99):
@@ -149,11 +154,14 @@ __device__ __forceinline__ float apply_act(float x, int act, float a, float b) {
             const float t = 1.f - 2.f * __builtin_amdgcn_rcpf(__expf(2.f * v) + 1.f);
             return 0.5f * x * (1.f + t);
         }
+        // IEEE quotients: past x = −87.3 the clamped 1 + e^(−x) exceeds 2^126, and
+        // the hardware reciprocal would flush 1/(1 + e^(−x)) to zero where the
+        // reference's quotient is subnormal (or, times a huge x, finite)
         case INGOT_ACT_SIGMOID: return 1.f / (1.f + exp_clamped(-x));
         case INGOT_ACT_SILU: return x / (1.f + exp_clamped(-x));
-        case INGOT_ACT_HARDSWISH: return x * clamp01(x / 6.f + 0.5f);
+        case INGOT_ACT_HARDSWISH: return x * clamp01(x * (1.f / 6.f) + 0.5f);
         case INGOT_ACT_HARDSIGMOID: return clamp01(a * x + b);
-        case INGOT_ACT_CLIP: return fminf(fmaxf(x, a), b);
+        case INGOT_ACT_CLIP: return clamp_to(x, a, b);
         case INGOT_ACT_LEAKYRELU: return x < 0.f ? x * a : x;
         default: return x;
     }

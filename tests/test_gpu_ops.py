@@ -291,6 +291,31 @@ def test_activation_nodes(sess, name, domain, attrs, code):
     assert_close(y, want, 2e-6 * max(1.0, float(np.max(np.abs(want)))), name)
 
 
+@pytest.mark.parametrize("code,a,b", [(L.ACT_RELU, 0, 0), (L.ACT_GELU_ERF, 0, 0), (L.ACT_GELU_TANH, 0, 0),
+                                      (L.ACT_SIGMOID, 0, 0), (L.ACT_SILU, 0, 0), (L.ACT_HARDSWISH, 0, 0),
+                                      (L.ACT_HARDSIGMOID, 0.2, 0.5), (L.ACT_CLIP, -1.5, 2.0), (L.ACT_LEAKYRELU, 0.1, 0)])
+def test_activation_special_values(sess, code, a, b):
+    """Every activation of the epilogue set on NaN, ±Inf, ±0, huge and exp-saturating inputs, against the
+    oracle: NaN where it gives NaN (the clamps of expScalar, clip and hardsigmoid compare, as Go's min/max do,
+    so a NaN passes through: kernels/vek/scalar.go:11-13, kernels/vek/vek_generic.go:48-76), the same ±Inf,
+    and finite values within 2e-6 relative."""
+    announce(f"activation special values act={code}")
+    special = [np.nan, np.inf, -np.inf, 0.0, -0.0, 1e30, -1e30, 3.4e38, -3.4e38, 100.0, -100.0, 88.5, -88.5,
+               87.4, -87.4, 20.0, -20.0, 1e-30, -1e-30, 0.5, -0.5, 3.0, -3.0]
+    x = np.array(special, np.float32).reshape(1, -1)
+    y = sess.empty(L.DT_F32, x.shape)
+    sess.activation(dev(sess, x), y, 1, x.shape[1], code, a=a, b=b)
+    got = y.numpy().astype(np.float64)
+    want = np.array([oracle.act(float(v), code, a, b) for v in x[0].astype(np.float64)]).reshape(x.shape)
+    want = want.astype(np.float32).astype(np.float64)  # the f32 the product would hold
+    assert np.array_equal(np.isnan(got), np.isnan(want)), f"NaN positions: got {got}, want {want}"
+    inf = np.isinf(want)
+    assert np.array_equal(np.isinf(got), inf) and np.array_equal(got[inf], want[inf]), f"Inf: got {got}, want {want}"
+    fin = np.isfinite(want)
+    err = np.abs(got[fin] - want[fin]) / np.maximum(1.0, np.abs(want[fin]))
+    assert err.max() <= 2e-6, f"act {code}: relative error {err.max():.3e} at {x[0][fin][np.argmax(err)]}"
+
+
 def test_refilled_weight_buffer_is_repacked(sess):
     """An operand not declared constant is packed per call: the same device buffer refilled with new values
     between runs gives the new product (Gemm f32 and bf16 B, MatMul, MatMulInteger). A declared-constant B
