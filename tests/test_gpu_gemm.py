@@ -547,15 +547,18 @@ def check_padded(got_full, want, n, tol, what, sentinel_bits=None):
 
 
 @pytest.mark.parametrize("pad", [3, 4])
-@pytest.mark.parametrize("route", ["f32", "bf16", "bf16x2", "gemv_m3", "gemv_m9", "gemm_m9", "bf16_y"])
+@pytest.mark.parametrize("route", ["f32", "bf16", "bf16x2", "gemv_m2", "gemv_m3", "gemv_m6", "gemv_m9", "gemm_m9",
+                                   "bf16_y", "gemv_m6_bf16_y"])
 def test_dirty_padded_destination(sess, route, pad):
     """The destination starts dirty (1e9 everywhere, as kernels/metal/gemmep_test.go:45-47) with row pitch
     ldy = N + pad: every output is overwritten and the padding past N stays untouched
     (kernels/metal/gemmep_test.go:22-96, kernels/metal/gemm_test.go:14,45). pad = 3 makes the pitch unaligned
-    (scalar stores), pad = 4 keeps 16-byte rows (vector stores)."""
+    (scalar stores), pad = 4 keeps 16-byte rows (vector stores). The GEMV routes: M = 2, 3 and 6 the LDS-DMA
+    kernel, M = 9 the MFMA kernel."""
     announce(f"dirty padded destination route={route} pad={pad}")
     rng = np.random.default_rng(len(route) * 101 + pad)
-    m, n, k = {"gemv_m3": (3, 300, 640), "gemv_m9": (9, 300, 640), "gemm_m9": (9, 4100, 512)}.get(route, (70, 197, 300))
+    m, n, k = {"gemv_m2": (2, 300, 640), "gemv_m3": (3, 300, 640), "gemv_m6": (6, 300, 640), "gemv_m9": (9, 300, 640),
+               "gemm_m9": (9, 4100, 512), "gemv_m6_bf16_y": (6, 300, 640)}.get(route, (70, 197, 300))
     a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
     bias = rng.normal(0, 0.1, n).astype(np.float32)
     kw = dict(beta=1.0, c=sess.to_device(bias), c_mode=L.C_ROW, act=L.ACT_GELU_ERF)
@@ -574,7 +577,7 @@ def test_dirty_padded_destination(sess, route, pad):
     want = oracle.gemm(np.ascontiguousarray(ain), bt, trans_b=True, c=bias, c_mode=L.C_ROW, beta=1.0,
                        act_code=L.ACT_GELU_ERF, **okw)
     tol = nstar_tol(k, a, wide)
-    if route == "bf16_y":
+    if route.endswith("bf16_y"):
         y, host = dirty_rows(sess, m, n, ldy, L.DT_BF16)
         sess.gemm(sess.to_device(a), w, y, m, ldy=ldy, **kw)
         got = y.numpy()
