@@ -266,7 +266,7 @@ hipError_t launch_rows(const A& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// ---- M <= 4: weight rows streamed through LDS by DMA ----
+// ---- M = 2..8: weight rows streamed through LDS by DMA ----
 // The rows kernel holds every in-flight weight chunk, and the activations that
 // go with it, in registers, which at M = 3..4 leaves one 512-k chunk per wave
 // in flight. Here the weight moves global → LDS by DMA (buffer_load_dwordx4
@@ -278,7 +278,9 @@ hipError_t launch_rows(const A& a, hipStream_t st) {
 // Persistent grid: wave g of G takes row groups g, g + G, ...; per row group
 // the FMAs run in the rows kernel's order (chunk by chunk, the same sequence)
 // and the same butterfly adds the lane partials, so y is bit-identical to it.
-// s_waitcnt vmcnt(V) expcnt(7) lgkmcnt(15) / vmcnt(63) expcnt(7) lgkmcnt(0)
+// wait_vm<V>: until at most V vector-memory operations of this wave are in
+// flight (s_waitcnt vmcnt(V), the other counters unconstrained); wait_lgkm0:
+// until its LDS operations have returned (lgkmcnt(0)).
 template <int V>
 __device__ __forceinline__ void wait_vm() {
     static_assert(V >= 0 && V < 64, "vmcnt is 6 bits");
