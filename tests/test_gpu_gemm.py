@@ -735,3 +735,61 @@ def test_random_shapes_all_kinds(sess, kind, seed):
     if kind == "f32" or m_small > 16:
         assert np.array_equal(run_gemm(sess, da, w, m_small, **kw), got[:m_small]), f"rows M={m_small} vs M={m}"
     w.free(), da.free(), db.free()
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_gemv_random_shapes(sess, seed):
+    """The decode routes on random shapes (kernels/gemm/bgemm.go:201-206): M from 1 to 16, N from 1 to ~6000
+    (odd included), K from 1 to ~7000 (K % 4 != 0 and rows past the LDS-staged length included), strided x,
+    a row bias and an activation, both math modes, through the GEMM entry (the router) and the GEMV entry.
+    Held to the north-star bound and, f32-class, the reference's relative 1e-5·sqrt(K); a second call is
+    bit-identical."""
+    rng = np.random.default_rng(8800 + seed)
+    m = int(rng.integers(1, 17))
+    n = int(rng.integers(1, 6000)) | (1 if seed % 2 else 0)
+    k = int(rng.integers(1, 7100)) if seed % 4 else int(rng.integers(1, 700)) * 4
+    lda = k + int(rng.integers(0, 9))
+    act = [L.ACT_NONE, L.ACT_RELU, L.ACT_GELU_ERF, L.ACT_SILU][seed % 4]
+    announce(f"gemv random seed={seed} m={m} n={n} k={k} lda={lda} act={act}")
+    xs = rng.normal(0, 1, (m, lda)).astype(np.float32)
+    x = xs[:, :k]
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    dx, db = sess.to_device(xs), sess.to_device(bias)
+    wide = oracle.bf16_to_f32(wb)
+    kw = dict(lda=lda, beta=1.0, c=db, c_mode=L.C_ROW, act=act)
+    for entry in (sess.gemm, sess.gemv_bf16):
+        for math_mode in (L.MATH_AUTO, L.MATH_BF16):
+            y = sess.empty(L.DT_F32, (m, n))
+            entry(dx, w, y, m, math=math_mode, **kw)
+            got = y.numpy()
+            xin = x if math_mode == L.MATH_AUTO else oracle.bf16_to_f32(oracle.f32_to_bf16(x))
+            want = oracle.gemm(np.ascontiguousarray(xin), wb, trans_b=True, b_dtype=oracle.BF16, c=bias,
+                               c_mode=L.C_ROW, beta=1.0, act_code=act)
+            what = f"{entry.__name__} math {math_mode}"
+            assert_close(got, want, nstar_tol(k, x, wide), what)
+            if math_mode == L.MATH_AUTO:
+                rel = np.max(np.abs(got - want)) / max(1.0, np.max(np.abs(want)))
+                assert rel <= 1e-5 * math.sqrt(k), f"{what}: relative error {rel:.3e}"
+            entry(dx, w, y, m, math=math_mode, **kw)
+            assert np.array_equal(y.numpy(), got), f"{what}: second call differs"
+    w.free(), dx.free(), db.free()
+
+
+@pytest.mark.parametrize("m", [1, 3, 4])
+def test_gemv_two_rows_per_wave_odd_n(env_session, m):
+    """The LDS-DMA GEMV with two weight rows per wave (INGOT_GEMV_CFG=26) where N is odd: the last wave's
+    second row is past N (its loads fill zeros, its sums are not stored)."""
+    announce(f"gemv two rows per wave odd n m={m}")
+    sess = env_session(INGOT_GEMV_CFG=26)
+    rng = np.random.default_rng(4200 + m)
+    n, k = 1001, 2048
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    y = sess.empty(L.DT_F32, (m, n))
+    sess.gemv_bf16(sess.to_device(x), w, y, m)
+    want = oracle.gemm(x, wb, trans_b=True, b_dtype=oracle.BF16)
+    assert_close(y.numpy(), want, nstar_tol(k, x, oracle.bf16_to_f32(wb)), f"cfg 26 m {m}")
+    w.free()
