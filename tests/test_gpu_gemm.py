@@ -644,6 +644,29 @@ def test_m_invariance(sess):
     wf.free(), wb.free(), da.free()
 
 
+@pytest.mark.parametrize("n,k", [(2048, 2048), (6144, 2048), (2048, 5632), (1000, 1300)])
+def test_gemv_rows_m_invariant(sess, n, k):
+    """The decode GEMV among itself: the M = 1 row kernel and the LDS-DMA kernel (M = 2..4 with K % 4 == 0 and
+    K <= 6144, and M = 5..8 with K <= 2048 and N < 4096) run the same FMA sequence per row and the same lane
+    butterfly, so a row is bit-identical whichever of these M carries it (the reference's GEMV is exempt at
+    M = 1; this keeps decode batches of 1..8 rows consistent with each other), in both math modes."""
+    announce(f"gemv rows m-invariance n={n} k={k}")
+    rng = np.random.default_rng(n + k)
+    x = rng.normal(0, 1, (8, k)).astype(np.float32)
+    wb = bf16_weights(rng, (n, k), 0.02, "normal")
+    w = sess.upload_weight(wb, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    dx = sess.to_device(x)
+    top = 8 if n < 4096 and k <= 2048 else 4
+    for kw in ({}, {"math": L.MATH_BF16}):
+        ys = {}
+        for m in range(1, top + 1):
+            y = sess.empty(L.DT_F32, (m, n))
+            sess.gemm(dx, w, y, m, **kw)
+            ys[m] = y.numpy()
+        for m in range(1, top):
+            assert np.array_equal(ys[m].view(np.uint32), ys[top][:m].view(np.uint32)), f"M={m} vs M={top} {kw}"
+    w.free(), dx.free()
+
 
 @pytest.mark.parametrize("seed", range(12))
 def test_hilo_random_shapes_and_row_invariance(sess, seed):
