@@ -137,11 +137,12 @@ def event_ms(sess, fn, reps: int) -> float:
 
 class Dit:
     name = "dit"
+    seed = 20260405  # numpy PCG64 (np.random.default_rng), recorded in the JSON line
     shapes = [(3072, 9216, "qkv"), (3072, 12288, "mlp_up_gelu"), (12288, 3072, "mlp_down")]
 
     def __init__(self, sess, L):
         self.sess, self.L = sess, L
-        rng = np.random.default_rng(20260405)
+        rng = np.random.default_rng(self.seed)
         self.M = 4096
         self.a = {k: sess.to_device(rng.normal(0, 1, (self.M, k)).astype(np.float32)) for k in (3072, 12288)}
         self.w, self.y, self.acts = [], [], []
@@ -239,7 +240,7 @@ class Dit:
         import torch
 
         L, s = self.L, self.sess
-        rng = np.random.default_rng(20260405)
+        rng = np.random.default_rng(self.seed)
         for (k, n, tag), act in zip(self.shapes, self.acts):
             a = rng.normal(0, 1, (self.M, k)).astype(np.float32)
             w = normal32(rng, (n, k), 0.02)
@@ -300,7 +301,7 @@ class Dit:
     def cpu_baseline(self, info, seconds: float):
         import oracle
 
-        rng = np.random.default_rng(20260405)
+        rng = np.random.default_rng(self.seed)
         rows = 288  # two MC blocks of the reference's blocking, per GEMM
         packs = [oracle.PackedB(oracle.f32_to_bf16(normal32(rng, (n, k), 0.02)), trans_b=True, bf16=True)
                  for k, n, _ in self.shapes]
@@ -323,9 +324,10 @@ class GemmRelu:
     A [128,256] ~U(-1,1), B [512,256] ~U(-1,1) (transB = 1), bias [512] ~N(0,0.1), ReLU fused into the store.
     33.6 MFLOP per call: launch-bound, so also reported as µs per call (HIP events, back-to-back calls)."""
     name = "gemm_relu"
+    seed = 7  # numpy PCG64 (np.random.default_rng), recorded in the JSON line
 
     def __init__(self, sess, L):
-        rng = np.random.default_rng(7)
+        rng = np.random.default_rng(self.seed)
         self.sess = sess
         self.M, self.K, self.N = 128, 256, 512
         a = sess.to_device(rng.uniform(-1, 1, (self.M, self.K)).astype(np.float32))
@@ -349,7 +351,7 @@ class GemmRelu:
         """The whole op on the host: packed-B f32 GEMM with the bias at the store, then the separate Relu node."""
         import oracle
 
-        rng = np.random.default_rng(7)
+        rng = np.random.default_rng(self.seed)
         a = rng.uniform(-1, 1, (self.M, self.K)).astype(np.float32)
         pb = oracle.PackedB(rng.uniform(-1, 1, (self.N, self.K)).astype(np.float32), trans_b=True, bf16=False)
         bias = rng.normal(0, 0.1, self.N).astype(np.float32)
@@ -366,11 +368,12 @@ class GemmRelu:
 
 class Bert:
     name = "bert"
+    seed = 1  # numpy PCG64 (np.random.default_rng), recorded in the JSON line
     shapes = [(768, 2304, 0), (768, 768, 0), (768, 3072, 1), (3072, 768, 0)]
 
     def __init__(self, sess, L):
         self.sess, self.L = sess, L
-        rng = np.random.default_rng(1)
+        rng = np.random.default_rng(self.seed)
         self.M = 1024
         self.a = {k: sess.to_device(rng.normal(0, 1, (self.M, k)).astype(np.float32)) for k in (768, 3072)}
         self.w, self.b, self.y = [], [], []
@@ -403,7 +406,7 @@ class Bert:
         strip on FFN-up (SgemmPackedBEpi)."""
         import oracle
 
-        rng = np.random.default_rng(1)
+        rng = np.random.default_rng(self.seed)
         a = {k: rng.normal(0, 1, (self.M, k)).astype(np.float32) for k in (768, 3072)}
         packs = [oracle.PackedB(rng.normal(0, 0.02, (k, n)).astype(np.float32), trans_b=False, bf16=False)
                  for k, n, _ in self.shapes]
@@ -421,10 +424,11 @@ class Bert:
 
 class Int8:
     name = "int8"
+    seed = 3  # numpy PCG64 (np.random.default_rng), recorded in the JSON line
 
     def __init__(self, sess, L):
         self.sess, self.L = sess, L
-        rng = np.random.default_rng(3)
+        rng = np.random.default_rng(self.seed)
         self.M, self.K, self.N = 1024, 768, 3072
         self.a = sess.to_device(rng.integers(0, 256, (self.M, self.K)).astype(np.uint8), L.DT_U8)
         self.w = sess.upload_weight(rng.integers(-127, 128, (self.K, self.N)).astype(np.int8), trans=False,
@@ -460,7 +464,7 @@ class Int8:
         pass (the reference's separate DequantizeLinear node)."""
         import oracle
 
-        rng = np.random.default_rng(3)
+        rng = np.random.default_rng(self.seed)
         a = rng.integers(0, 256, (self.M, self.K)).astype(np.uint8)
         bt = np.ascontiguousarray(rng.integers(-127, 128, (self.K, self.N)).astype(np.int8).T)
         sc = (rng.uniform(0.001, 0.01, self.N).astype(np.float32) * np.float32(0.02)).astype(np.float32)
@@ -478,12 +482,13 @@ class Int8:
 
 class Decode:
     name = "decode"
+    seed = 4  # numpy PCG64 (np.random.default_rng), recorded in the JSON line
     shapes = [(2048, 6144), (2048, 2048), (2048, 11264), (5632, 2048)]
     copies = 3  # > 256 MB of weights in rotation: HBM, not the Infinity Cache
 
     def __init__(self, sess, L, M=1):
         self.sess, self.L, self.M = sess, L, M
-        rng = np.random.default_rng(4)
+        rng = np.random.default_rng(self.seed)
         self.x = {k: sess.to_device(rng.normal(0, 1, (16, k)).astype(np.float32)) for k in (2048, 5632)}
         self.w = [[sess.upload_weight(normal32(rng, (n, k), 0.02), trans=True, pack_dtype=L.DT_BF16)
                    for k, n in self.shapes] for _ in range(self.copies)]
@@ -549,7 +554,7 @@ class Decode:
         out["m1_per_shape"] = per
         # the same step on grouped-int8 weights (ingot_weight_quant="int8"): bytes = int8 weights + f32 scales
         L = self.L
-        wq = [[self.sess.upload_weight(normal32(np.random.default_rng(5 + c), (n, k), 0.02), trans=True,
+        wq = [[self.sess.upload_weight(normal32(np.random.default_rng(self.seed + 1 + c), (n, k), 0.02), trans=True,
                                        pack_dtype=L.PACK_I8G) for k, n in self.shapes] for c in range(self.copies)]
         i = [0]
 
@@ -574,7 +579,7 @@ class Decode:
         """The M = 1 decode step on the host: the four bf16-weight GEMVs with a widening dot (GemvBF16)."""
         import oracle
 
-        rng = np.random.default_rng(4)
+        rng = np.random.default_rng(self.seed)
         xs = {k: rng.normal(0, 1, (1, k)).astype(np.float32) for k in (2048, 5632)}
         ws = [oracle.f32_to_bf16(normal32(rng, (n, k), 0.02)) for k, n in self.shapes]
 
@@ -592,6 +597,7 @@ class FfnGraph:
     """BERT FFN block (configs[1] shapes) as a graph session: MatMul+Add → GELU → MatMul+Add, planned with
     fuseMatMulBias + epilogue activations in f32, and under GPUBF16 (bf16 products, bf16-resident hidden)."""
     name = "ffn_graph"
+    seed = 6  # numpy PCG64 (np.random.default_rng), recorded in the JSON line
     TEXT = """
 input x f32 1024,768
 const W1 f32 768,3072
@@ -609,7 +615,7 @@ output y
     def __init__(self, sess, L):
         from ingot_amd import Graph
         self.sess, self.L = sess, L
-        rng = np.random.default_rng(6)
+        rng = np.random.default_rng(self.seed)
         self.x = sess.to_device(rng.normal(0, 1, (1024, 768)).astype(np.float32))
         self.c = {"W1": normal32(rng, (768, 3072), 0.02), "b1": normal32(rng, (3072,), 0.02),
                   "W2": normal32(rng, (3072, 768), 0.02), "b2": normal32(rng, (768,), 0.02)}
@@ -689,7 +695,8 @@ def main() -> int:
                     "config": {"workload": "DiT/QwenImage transformer GEMMs (BASELINE configs[4])", "M": 4096,
                                "gemms": ["3072x9216", "3072x12288+gelu", "12288x3072"],
                                "activations": "f32, bf16 RNE on load", "weights": "bf16", "accumulate": "f32",
-                               "global_batch": 4096, "parallelism": "none (1 GPU)"}})
+                               "global_batch": 4096, "parallelism": "none (1 GPU)", "seed": Dit.seed,
+                               "prng": "numpy PCG64 (np.random.default_rng)"}})
         log(f"dit: {res['value']} TFLOPS, {ms:.3f} ms/step; kernel roofline")
         res["roofline"] = wl.kernel_roofline()
         log("dit: default-math (hi/lo) step")
@@ -703,28 +710,31 @@ def main() -> int:
         if args.workload == "decode":
             rep = wl.report()
             res.update({"value": rep["m1"]["GB_per_s"], "unit": "GB/s", "ms_per_step": rep["m1"]["us_per_step"] / 1e3,
-                        "dtype": "bf16", "config": {"workload": "decode GEMV M=1 (BASELINE configs[3])"},
+                        "dtype": "bf16", "config": {"workload": "decode GEMV M=1 (BASELINE configs[3])", "seed": wl.seed},
                         "detail": rep})
         else:
             ms = time_steps(sess, wl.step, args.steps, args.warmup)
             rep = wl.report(ms)
             res.update({"value": rep["value"], "unit": rep["unit"], "ms_per_step": rep["ms_per_step"],
-                        "dtype": rep["dtype"], "config": {"workload": args.workload}, "detail": rep})
+                        "dtype": rep["dtype"], "config": {"workload": args.workload, "seed": wl.seed}, "detail": rep})
     if args.workload == "dit" and not args.no_extra:
         extra = {}
         for cls in (GemmRelu, Bert, Int8):
             log(f"{cls.name}: measuring")
             w = cls(sess, L)
             extra[cls.name] = w.report(time_steps(sess, w.step, 50, 10))
+            extra[cls.name]["seed"] = cls.seed
             if info:
                 extra[cls.name]["cpu_baseline"] = w.cpu_baseline(info, args.cpu_seconds_extra)
         log("decode: measuring")
         dec = Decode(sess, L)
         extra["decode"] = dec.report()
+        extra["decode"]["seed"] = Decode.seed
         if info:
             extra["decode"]["cpu_baseline"] = dec.cpu_baseline(info, args.cpu_seconds_extra)
         log("ffn graph: measuring")
         extra["ffn_graph"] = FfnGraph(sess, L).report()
+        extra["ffn_graph"]["seed"] = FfnGraph.seed
         res["workloads"] = extra
     sess.close()
     print(json.dumps(res), flush=True)
