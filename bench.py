@@ -499,6 +499,57 @@ class Decode:
         self.calls = {M: [[sess.prepare_gemm(self.x[k], w, y, M) for (k, n), w, y in zip(self.shapes, ws, self.y)]
                           for ws in self.w] for M in (1, 4, 16)}
 
+    def compare_stream_read(self, reps: int = 20):
+        """The M = 1 GEMV of each decode shape against reading the same weight bytes with vendor code: a
+        torch.sum over a bf16 tensor of the weight's shape (torch's reduction kernel, f32 accumulation), and a
+        device-to-device torch copy of the same bytes (which also writes them). Each side rotates over
+        `copies` distinct buffers (beyond the Infinity Cache together), timed with HIP events over `reps`
+        launches, four alternating rounds; the minimum of each is compared. One JSON line per shape."""
+        import torch
+
+        s = self.sess
+        rng = np.random.default_rng(self.seed)
+        for j, (k, n) in enumerate(self.shapes):
+            tw = [torch.from_numpy(normal32(rng, (n, k), 0.02)).to("cuda").to(torch.bfloat16)
+                  for _ in range(self.copies)]
+            dst = torch.empty_like(tw[0])
+
+            def ours():
+                for c in range(self.copies):
+                    self.calls[1][c][j]()
+
+            def torch_ms(fn):
+                fn()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(reps):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1) / reps
+
+            def tsum():
+                for t in tw:
+                    torch.sum(t, dtype=torch.float32)
+
+            def copy():
+                for t in tw:
+                    dst.copy_(t)
+
+            g, r, cp = [], [], []
+            for _ in range(4):
+                g.append(event_ms(s, ours, reps) / self.copies * 1e3)
+                r.append(torch_ms(tsum) / self.copies * 1e3)
+                cp.append(torch_ms(copy) / self.copies * 1e3)
+            wb = 2.0 * n * k
+            print(json.dumps({"shape": f"{k}x{n}", "weight_MB": round(wb / 1e6, 2),
+                              "gemv_m1_us": round(min(g), 2), "gemv_m1_GB_per_s": round(wb / min(g) / 1e3, 1),
+                              "torch_sum_us": round(min(r), 2), "torch_sum_GB_per_s": round(wb / min(r) / 1e3, 1),
+                              "d2d_copy_us": round(min(cp), 2), "d2d_copy_read_GB_per_s": round(wb / min(cp) / 1e3, 1)}),
+                  flush=True)
+            del tw, dst
+
     def bytes_step(self, M):
         return self.wbytes + sum(4.0 * M * (k + n) for k, n in self.shapes)
 
@@ -656,17 +707,20 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU-baseline time budget of the DiT leg")
     ap.add_argument("--cpu-seconds-extra", type=float, default=3.0,
                     help="CPU-baseline time budget of each other workload")
-    ap.add_argument("--probe", nargs="?", const="dit", choices=["dit", "decode", "bert", "int8", "hipblaslt"],
+    ap.add_argument("--probe", nargs="?", const="dit",
+                    choices=["dit", "decode", "bert", "int8", "hipblaslt", "streamread"],
                     help="counter probe for rocprofv3 --pmc: one calibration copy, then one launch of each DiT GEMM "
                          "(dit, the default) or one decode GEMV step at M = 1, 4, 16 (decode); bert: one launch of "
                          "each BERT f32 projection; int8: one calibration copy, then one MatMulInteger + dequant call; "
-                         "hipblaslt: the DiT GEMM kernel against hipBLASLt on the same operands (one JSON line each)")
+                         "hipblaslt: the DiT GEMM kernel against hipBLASLt on the same operands (one JSON line each); "
+                         "streamread: the M = 1 decode GEMVs against a vendor read (torch.sum) and a device copy of the "
+                         "same weight bytes (one JSON line each)")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU (the path has no multi-GPU component); run with --gpus 1")
         return 2
 
-    if args.probe == "hipblaslt":
+    if args.probe in ("hipblaslt", "streamread"):
         # torch's HIP runtime is loaded and initialised before the library's (started the other way round,
         # torch finds no GPU)
         import torch
@@ -678,6 +732,10 @@ def main() -> int:
     sess = Session(0)
     if args.probe == "hipblaslt":
         Dit(sess, L).compare_hipblaslt()
+        sess.close()
+        return 0
+    if args.probe == "streamread":
+        Decode(sess, L).compare_stream_read()
         sess.close()
         return 0
     if args.probe:
