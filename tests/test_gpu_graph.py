@@ -136,3 +136,70 @@ def test_graph_dynamic_rhs_packed_per_run(sess):
         err = np.max(np.abs(got - want)) / max(1.0, np.max(np.abs(want)))
         assert err <= 1e-5 * math.sqrt(k), f"run {run}: relative error {err:.3e}"
     g.free()
+
+
+def _session_work(seed, runs):
+    """One thread's work on a session of its own: the MLP graph under both plans and a decode GEMV, `runs`
+    times each; returns every output."""
+    from ingot_amd import Session
+
+    s = Session(0)
+    try:
+        text, dev, x, _ = mlp_case(s, m=64, seed=seed)
+        graphs = []
+        for flags in (L.GRAPH_FUSE_BIAS | L.GRAPH_FUSE_ACT, L.GRAPH_FUSE_BIAS | L.GRAPH_FUSE_ACT | L.GRAPH_HALF):
+            g = Graph(s, text)
+            for k, v in dev.items():
+                g.bind(k, v)
+            g.compile(flags)
+            graphs.append(g)
+        rng = np.random.default_rng(seed)
+        xv = s.to_device(rng.normal(0, 1, (4, 2048)).astype(np.float32))
+        w = s.upload_weight(rng.normal(0, 0.02, (3000, 2048)).astype(np.float32), trans=True, pack_dtype=L.DT_BF16)
+        yv = s.empty(L.DT_F32, (4, 3000))
+        outs = []
+        for _ in range(runs):
+            for g in graphs:
+                (y,) = g.run({"x": x})
+                outs.append(y.numpy())
+                y.free()
+            s.gemm(xv, w, yv, 4)
+            outs.append(yv.numpy())
+        for g in graphs:
+            g.free()
+        w.free()
+        return outs
+    finally:
+        s.close()
+
+
+def test_sessions_run_concurrently():
+    """TestSessionConcurrentRun (graph/concurrent_test.go:18) for this backend: one session serialises its own
+    calls (a single stream; GPUSession.runMu, graph/gpu_darwin_arm64.go:308), so concurrency is a session per
+    thread. Four threads, each with its own session, compiled MLP graphs (f32 and GPUBF16 plans) and an M = 4
+    decode GEMV, run at once (the library calls release the interpreter lock); every output is bit-identical
+    to the same work run alone."""
+    import threading
+
+    announce("sessions on four threads")
+    seeds, runs = [31, 32, 33, 34], 6
+    alone = {sd: _session_work(sd, runs) for sd in seeds}
+    got, errs = {}, []
+
+    def worker(sd):
+        try:
+            got[sd] = _session_work(sd, runs)
+        except Exception as e:  # reported below, in the test's thread
+            errs.append(f"seed {sd}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(sd,)) for sd in seeds]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=100)
+    assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
+    assert not errs, errs
+    for sd in seeds:
+        assert len(got[sd]) == len(alone[sd])
+        for i, (a, b) in enumerate(zip(got[sd], alone[sd])):
+            assert a.dtype == b.dtype and a.tobytes() == b.tobytes(), f"seed {sd}: output {i} differs"
