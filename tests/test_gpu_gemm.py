@@ -67,6 +67,42 @@ def test_gemm_bf16_weights(sess, m, n, k):
     w.free(), da.free()
 
 
+@pytest.mark.parametrize("m,n,k", [(70, 197, 300), (1, 1000, 1300), (4, 3001, 2048), (300, 513, 2100)])
+def test_bf16_pack_sources_agree(sess, m, n, k):
+    """TestPackBBF16's property (kernels/gemm/packbf16_test.go:13: the bf16 pack is bit-identical whatever
+    route built it, products included) for this library's pack: the same weight uploaded as f32 (rounded by
+    the library, F32ToBF16 RNE) or as bf16 bits rounded on the host by the oracle, each as [N,K] (transB) or
+    [K,N], gives bit-identical products in both math modes, through the GEMM and, at M <= 4, the GEMV. A
+    fifth of the f32 values sit exactly halfway between two bf16 values, so the library's round-to-nearest-
+    even must break ties as F32ToBF16 does."""
+    announce(f"bf16 pack sources m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 17 + n * 3 + k)
+    w32 = rng.normal(0, 0.05, (n, k)).astype(np.float32)
+    bits = w32.view(np.uint32)
+    tie = rng.random((n, k)) < 0.2
+    bits[tie] = (bits[tie] & np.uint32(0xFFFF0000)) | np.uint32(0x8000)
+    w16 = oracle.f32_to_bf16(w32)
+    ah = rng.normal(0, 1, (m, k)).astype(np.float32)
+    a = sess.to_device(ah)
+    uploads = [sess.upload_weight(w32, trans=True, pack_dtype=L.DT_BF16),
+               sess.upload_weight(w16, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16),
+               sess.upload_weight(np.ascontiguousarray(w32.T), trans=False, pack_dtype=L.DT_BF16),
+               sess.upload_weight(np.ascontiguousarray(w16.T), trans=False, pack_dtype=L.DT_BF16,
+                                  src_dtype=L.DT_BF16)]
+    first = None
+    for kw in ({}, {"math": L.MATH_BF16}):
+        ys = [run_gemm(sess, a, w, m, **kw) for w in uploads]
+        for i, y in enumerate(ys[1:], 1):
+            assert np.array_equal(y.view(np.uint32), ys[0].view(np.uint32)), f"upload {i} differs {kw}"
+        first = ys[0] if first is None else first
+    # and the default-math product against the float64 oracle on the host-rounded weight
+    want = oracle.gemm(ah, w16, trans_b=True, b_dtype=oracle.BF16)
+    assert_close(first, want, nstar_tol(k, ah, oracle.bf16_to_f32(w16)), "bf16 pack vs oracle")
+    for w in uploads:
+        w.free()
+    a.free()
+
+
 @pytest.mark.parametrize("m,n,k", SHAPES)
 def test_gemm_bf16_math_rounds_activations(sess, m, n, k):
     """INGOT_MATH_BF16 (GPUBF16 semantics): A rounded to bf16 once; exact up to f32 accumulation."""
