@@ -136,6 +136,32 @@ def test_gemm_alpha_beta_c_modes(sess, mode, pack):
     assert_close(got, want, nstar_tol(k, a, bw) + 1e-6, f"C mode {mode}")
 
 
+@pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (1.0, 1.0), (0.5, 0.0), (2.0, -0.5)])
+@pytest.mark.parametrize("pack", [L.DT_F32, L.DT_BF16])
+@pytest.mark.parametrize("m,n,k", [(1, 70, 130), (45, 70, 130), (300, 257, 515)])
+def test_gemm_alpha_beta_combos(sess, alpha, beta, pack, m, n, k):
+    """TestSgemmMatchesRef's α/β combinations (kernels/gemm/gemm_test.go:47) with a full C operand, held to the
+    reference's f32 tolerance (relative 1e-5·sqrt(K), kernels/gemm/gemm_test.go:34) against the float64 oracle,
+    on the GEMV (M = 1, bf16) and GEMM routes; β = 0 must ignore C even where it holds NaN."""
+    announce(f"gemm alpha={alpha} beta={beta} pack={pack} m={m}")
+    rng = np.random.default_rng(int(alpha * 10) + int((beta + 1) * 100) + pack * 7 + m)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    c = rng.normal(size=(m, n)).astype(np.float32)
+    if beta == 0.0:
+        c[::3, ::5] = np.nan
+    w = sess.upload_weight(bt, trans=True, pack_dtype=pack)
+    got = run_gemm(sess, sess.to_device(a), w, m, alpha=alpha, beta=beta, c=sess.to_device(c), c_mode=L.C_FULL,
+                   ldc=n)
+    bw = bt if pack == L.DT_F32 else oracle.bf16_to_f32(oracle.f32_to_bf16(bt))
+    cz = np.where(np.isnan(c), 0, c).astype(np.float32) if beta == 0.0 else c
+    want = oracle.gemm(a, bw, trans_b=True, alpha=alpha, beta=beta, c=cz, c_mode=L.C_FULL, ldc=n)
+    assert not np.isnan(got).any()
+    rel = np.max(np.abs(got - want) / np.maximum(np.abs(want), 1.0))
+    assert rel <= 1e-5 * math.sqrt(k), f"relative error {rel:.3e}"
+    w.free()
+
+
 @pytest.mark.parametrize("act,aa,ab", [(L.ACT_RELU, 0, 0), (L.ACT_GELU_ERF, 0, 0), (L.ACT_GELU_TANH, 0, 0),
                                        (L.ACT_SIGMOID, 0, 0), (L.ACT_SILU, 0, 0), (L.ACT_HARDSWISH, 0, 0),
                                        (L.ACT_HARDSIGMOID, 0.2, 0.5), (L.ACT_CLIP, -0.5, 0.7),
