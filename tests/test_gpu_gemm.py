@@ -302,6 +302,27 @@ def test_gemv_i8g_rows_per_wave(env_session, rows, m):
     w.free()
 
 
+def test_operands_past_2gib_decline(sess):
+    """Every GEMM operand is addressed with 32-bit buffer offsets, so an A operand whose extent reaches 2 GiB is
+    declined (INGOT_EDECLINED: the caller runs the CPU op) before anything is launched or allocated; the buffers
+    here are real and large enough, so even a launch would stay in bounds. A smaller call on them runs."""
+    announce("2 GiB decline")
+    k, n = 4096, 8
+    m = (1 << 31) // (2 * k) + 1  # bf16 rows of 8 KiB: the extent passes 2^31 bytes
+    rng = np.random.default_rng(12)
+    w = sess.upload_weight(rng.normal(0, 0.02, (n, k)).astype(np.float32), trans=True, pack_dtype=L.DT_BF16)
+    a = sess.empty(L.DT_BF16, (m, k))
+    y = sess.empty(L.DT_F32, (m, n))
+    with pytest.raises(IngotError) as e:
+        sess.gemm(a, w, y, m, a_dtype=L.DT_BF16)
+    assert e.value.code == L.EDECLINED and "2 GiB" in str(e.value)
+    small = 1024
+    sess.memset(a, 0)
+    sess.gemm(a, w, y, small, a_dtype=L.DT_BF16)
+    assert not y.numpy()[:small].any()
+    a.free(), y.free(), w.free()
+
+
 def test_gemv_i8g_declines_prefill(sess):
     """An int8 (I8G) weight serves decode only: M > 16 is declined (the caller keeps its bf16 path)."""
     announce("i8g declines")
