@@ -199,7 +199,7 @@ class Dit:
         achieved = flops / (ms * 1e-3) / 1e12
         return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK["bf16"], "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK["bf16"], 4), "traffic": measured_traffic(),
-                "kernel": "gemm_kernel<bf16> (256x192 for QKV and MLP-down, 256x256 for MLP-up)",
+                "kernel": "gemm_kernel<bf16> (256x192 for QKV, 256x256 for MLP-up, 256x192 with register-staged weights for MLP-down)",
                 "avg_launch_us": round(ms * 1e3, 2),
                 "flops_per_launch": flops,
                 "zero_operands": self.zero_operand_rate()}

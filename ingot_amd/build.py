@@ -28,7 +28,7 @@ COMMON = [
     "-Wall",
     "-Wno-unused-function",
 ]
-SOURCES = ["gemm_mfma.hip", "gemv_bf16.hip", "gemv_i8g.hip", "qconv.hip", "elementwise.hip", "runtime.cpp", "ops.cpp", "graph.cpp"]
+SOURCES = ["gemm_bf16x2.hip", "gemm_bf16.hip", "gemm_f32.hip", "gemm_i8.hip", "gemm_mfma.hip", "gemv_bf16.hip", "gemv_i8g.hip", "qconv.hip", "elementwise.hip", "runtime.cpp", "ops.cpp", "graph.cpp"]
 
 
 def hipcc() -> str:

@@ -1,5 +1,5 @@
 // Internal launch interface between the runtime (runtime.cpp) and the gfx950
-// kernels (gemm_mfma.hip, gemv_bf16.hip, elementwise.hip).
+// kernels (gemm_mfma.hpp and its per-kind units, gemv_bf16.hip, elementwise.hip).
 #pragma once
 
 #include "common.hpp"
@@ -55,9 +55,10 @@ struct GemmArgsQ : GemmCore {
 
 struct GemmConfig {
     int bm, bn;
-    int occupancy;   // workgroups per CU the tile allows
+    int occupancy;   // workgroups per CU the tile allows (eff 0: never picked by itself)
     float eff;       // relative per-CU efficiency (tile-size heuristic)
     bool one_round;  // only when every tile is resident at once (a latency-bound shape)
+    int deep = -1;   // index of the same tile with loads issued two k-tiles ahead (operands from HBM)
 };
 
 // Tile configurations compiled for `kind`; index used by launch_gemm.

@@ -53,6 +53,10 @@ int elem_size(int dt) {
     return 0;
 }
 
+// Operand bytes above which a GEMM's operands are taken not to stay in the
+// Infinity Cache between uses: half of its 256 MB on MI355X.
+constexpr int64_t kCacheResidentBytes = (int64_t)128 << 20;
+
 // elements of a kind per 128-byte k-tile
 int ktile_elems(GemmKind k) { return k == KIND_F32 ? 32 : (k == KIND_I8 ? 128 : 64); }
 int kind_size(GemmKind k) { return k == KIND_F32 ? 4 : (k == KIND_I8 || k == KIND_I8G ? 1 : 2); }
@@ -68,6 +72,7 @@ int pick_config(GemmKind kind, int64_t M, int64_t N, int64_t batch, int num_cus,
     int best = 0;
     double best_t = 1e300;
     for (int i = 0; i < n; ++i) {
+        if (c[i].eff <= 0.f) continue;  // reached only as another entry's deep variant
         const int64_t tiles = ((M + c[i].bm - 1) / c[i].bm) * ((N + c[i].bn - 1) / c[i].bn) * batch;
         const int64_t slots = (int64_t)num_cus * c[i].occupancy;
         const int64_t rounds = (tiles + slots - 1) / slots;
@@ -649,9 +654,15 @@ static int gemm_core(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const
     g.y = a->d_y;
     g.ldy = a->ldy;
     g.epi = make_epi(a);
-    const int cfg = pick_config(kind, a->M, a->N, batch, s->num_cus, s->force_gemm_cfg);
+    int cfg = pick_config(kind, a->M, a->N, batch, s->num_cus, s->force_gemm_cfg);
     const GemmConfig* c;
     gemm_configs(kind, &c);
+    // Operands larger than half the Infinity Cache (256 MB on MI355X) do not
+    // stay cached between uses: the product's own output and its neighbours'
+    // evict them, so they come from HBM, where the tile whose loads are issued
+    // two k-tiles ahead is faster (the configuration tables give the figures).
+    if (s->force_gemm_cfg < 0 && c[cfg].deep >= 0 && batch * a_extent + b_extent > kCacheResidentBytes)
+        cfg = c[cfg].deep;
     g.tiles_m = (int)((a->M + c[cfg].bm - 1) / c[cfg].bm);
     g.tiles_n = (int)((a->N + c[cfg].bn - 1) / c[cfg].bn);
     hipError_t e = launch_gemm(kind, cfg, g, (int)batch, s->stream);

@@ -384,7 +384,7 @@ def test_gemv_epilogue(sess, m):
 # ragged edges in M, N and K, with a bias and an activation in the epilogue
 # (int8: the column-sum correction and fused dequantisation). Indices follow the
 # configuration tables of gemm_mfma.hip.
-GEMM_CFGS = {"f32": range(6), "bf16": range(9), "bf16x2": range(9), "i8": range(6)}
+GEMM_CFGS = {"f32": range(6), "bf16": range(10), "bf16x2": range(10), "i8": range(6)}
 
 
 @pytest.mark.parametrize("kind,cfg", [(k, c) for k, r in GEMM_CFGS.items() for c in r])
@@ -725,6 +725,28 @@ def test_m_invariance(sess):
         for M in (5, 9, 16, 17, 40, 129, 300):
             assert np.array_equal(rows_of(wb, n, M, **kw), full[:M]), f"bf16 weights M={M} {kw}"
     wf.free(), wb.free(), da.free()
+
+
+def test_deep_prefetch_tile_m_invariant(env_session):
+    """The 256×192 tile with the weight staged through registers (taken for products whose operands are too large
+    to stay in the Infinity Cache) reduces K in the tile kinds' common order: its rows are bit-identical to the rows
+    the other tiles give at smaller M, for bf16 A and for the hi/lo split, K over several k-tiles and ragged."""
+    announce("deep-prefetch tile m invariance")
+    rng = np.random.default_rng(77)
+    m, n, k = 600, 1000, 1333
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wt = bf16_weights(rng, (n, k), 0.05, "normal")
+    deep, plain = env_session(INGOT_GEMM_CFG=9), env_session(INGOT_GEMM_CFG=-1)
+    for kw in ({}, {"math": L.MATH_BF16}):
+        rows = {}
+        for name, s, M in (("deep", deep, m), ("plain", plain, 17), ("plain", plain, 300)):
+            w = s.upload_weight(wt, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+            y = s.empty(L.DT_F32, (M, n))
+            s.gemm(s.to_device(a[:M]), w, y, M, **kw)
+            rows[(name, M)] = y.numpy()
+            w.free()
+        for M in (17, 300):
+            assert np.array_equal(rows[("plain", M)], rows[("deep", m)][:M]), f"deep tile rows differ at M={M} {kw}"
 
 
 @pytest.mark.parametrize("n,k", [(2048, 2048), (6144, 2048), (2048, 5632), (1000, 1300)])

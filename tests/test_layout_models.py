@@ -3,7 +3,7 @@ kernels/gemm/qgemm_test.go:122,225: model the contract of code the test machine 
 layout plumbing everywhere; the kernels themselves are tested on the GPU).
 
 Each model follows the index arithmetic of one kernel and checks a property that kernel relies on:
-- gemm_mfma.hip: the LDS chunk swizzle of the DMA ring pairs the same 16-byte k chunk of A and B in every
+- gemm_mfma.hpp: the LDS chunk swizzle of the DMA ring pairs the same 16-byte k chunk of A and B in every
   MFMA fragment, and the 16 rows a ds_read_b128 phase reads fall on 16 distinct 16-byte bank groups;
 - gemv_bf16.hip reduce_store: the reduce-scatter butterfly gives every sum bit-identical to a full butterfly,
   and exactly one store lane holds each sum;
