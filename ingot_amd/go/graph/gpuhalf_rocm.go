@@ -4,101 +4,118 @@ package graph
 
 import "github.com/giraffesyo/ingot/kernels/rocm"
 
-// GPUBF16 plan of the rocm session, the planHalf of the Metal session
-// (graph/gpuhalf_darwin_arm64.go:29-112) restated for this backend's ops:
+// The GPUBF16 plan of the rocm session: the decisions of the Metal session's
+// planHalf (graph/gpuhalf_darwin_arm64.go:29-112), made here over this
+// backend's ops.
 //
-//   - a matrix product against a constant weight whose only consumer is an
-//     activation node applies that activation in its store (fuseAct), and
-//     the activation node passes its input through (actStep);
-//   - a value read only by bf16 products against constant weights (as
-//     their A operand, possibly through views) is produced in bf16 on the
-//     device (halfOut): one f32 → bf16 pass less per consumer, the same
-//     rounding the consumer's cast applies, so results do not change.
+//   - A matrix product against a constant weight whose output has exactly
+//     one reader, an activation node reading it as its input, applies that
+//     activation in its store (fuseAct); the activation node then passes its
+//     input through (actStep).
+//   - A value may live on the device as bf16 when it is not a graph output,
+//     has readers, and every reader takes bf16 anyway: a product against a
+//     constant weight reading it as its A operand, or a view whose own
+//     output may live as bf16. Such a value is stored in bf16 by its
+//     producer (halfOut): the rounding its readers' casts would apply, so
+//     results do not change, and one f32 write and read less.
 //
 // A CPU node that reads such a value gets it widened back to f32 when it is
 // downloaded (GPUSession.toHost).
 func (s *GPUSession) planHalf() {
-	type use struct{ step, slot int }
-	users := make([][]use, s.nval)
-	for i, st := range s.steps {
-		for k, id := range st.in {
+	n := len(s.steps)
+	s.fuseAct, s.actStep, s.halfOut = make([]int, n), make([]bool, n), make([]bool, n)
+
+	// Reader census: how many (step, slot) reads each value has, and the
+	// last of them (the only one when the count is 1).
+	reads := make([]int, s.nval)
+	lastStep, lastSlot := make([]int, s.nval), make([]int, s.nval)
+	for j := range s.steps {
+		for k, id := range s.steps[j].in {
 			if id >= 0 {
-				users[id] = append(users[id], use{i, k})
+				reads[id]++
+				lastStep[id], lastSlot[id] = j, k
 			}
 		}
 	}
-	n := len(s.steps)
-	s.fuseAct, s.actStep, s.halfOut = make([]int, n), make([]bool, n), make([]bool, n)
-	out0 := func(i int) int {
-		if st := &s.steps[i]; len(st.out) > 0 {
-			return st.out[0]
+	firstOut := func(j int) int {
+		if out := s.steps[j].out; len(out) > 0 {
+			return out[0]
 		}
 		return -1
 	}
-	constWeight := func(st *step) bool {
-		if len(st.in) < 2 || st.in[1] < 0 {
+	// bf16Product: step j is a matrix product whose A operand the bf16 math
+	// takes, against a constant 2-D contiguous weight (input 1).
+	bf16Product := func(j int) bool {
+		switch g := s.gops[j].(type) {
+		case gemmGPU:
+			if g.transA || g.quantI8 {
+				return false
+			}
+		case matmulGPU:
+			if g.act != rocm.ActNone {
+				return false
+			}
+		default:
 			return false
 		}
-		w := s.constVals[st.in[1]]
+		in := s.steps[j].in
+		if len(in) < 2 || in[1] < 0 {
+			return false
+		}
+		w := s.constVals[in[1]]
 		return w != nil && w.Shape().Rank() == 2 && w.IsContiguous()
 	}
-	product := func(i int) bool {
-		switch g := s.gops[i].(type) {
-		case gemmGPU:
-			return !g.transA && !g.quantI8
-		case matmulGPU:
-			return g.act == rocm.ActNone
-		}
-		return false
-	}
-	for i := range s.steps {
-		st := &s.steps[i]
-		id := out0(i)
-		if !product(i) || !constWeight(st) || id < 0 || s.isOutput[id] || len(users[id]) != 1 || users[id][0].slot != 0 {
+
+	for j := range s.steps {
+		v := firstOut(j)
+		if v < 0 || s.isOutput[v] || reads[v] != 1 || lastSlot[v] != 0 || !bf16Product(j) {
 			continue
 		}
-		u := users[id][0].step
-		if a, ok := s.gops[u].(unaryGPU); ok && out0(u) >= 0 {
-			s.fuseAct[i], s.actStep[u] = a.act, true
+		u := lastStep[v]
+		if a, ok := s.gops[u].(unaryGPU); ok && firstOut(u) >= 0 {
+			s.fuseAct[j] = a.act
+			s.actStep[u] = true
 		}
 	}
-	// want[id]: 0 unknown, 1 every consumer reads bf16, 2 not
-	want := make([]int8, s.nval)
-	var wants func(id int) bool
-	reads := func(u use) bool {
-		st := &s.steps[u.step]
-		if st.node.Domain == "" && viewOps[st.node.OpType] {
-			return u.slot == 0 && out0(u.step) >= 0 && wants(out0(u.step))
-		}
-		return u.slot == 0 && product(u.step) && constWeight(st) && !s.actStep[u.step]
+
+	// halfOK[v]: value v may live as bf16. Every reader of a value comes
+	// after its producer in the step order, so sweeping the steps backwards
+	// settles a view's output before the view's own input is examined: each
+	// read that does not take bf16 vetoes the value it reads.
+	halfOK := make([]bool, s.nval)
+	for v := range halfOK {
+		halfOK[v] = reads[v] > 0 && !s.isOutput[v]
 	}
-	wants = func(id int) bool {
-		if want[id] == 0 {
-			want[id] = 2 // provisional, ends cycles
-			ok := !s.isOutput[id] && len(users[id]) > 0
-			for _, u := range users[id] {
-				if !ok {
-					break
+	for j := n - 1; j >= 0; j-- {
+		st := &s.steps[j]
+		isView := st.node.Domain == "" && viewOps[st.node.OpType]
+		for k, v := range st.in {
+			if v < 0 || !halfOK[v] {
+				continue
+			}
+			takes := false
+			if k == 0 {
+				if isView {
+					w := firstOut(j)
+					takes = w >= 0 && halfOK[w]
+				} else {
+					takes = bf16Product(j) && !s.actStep[j]
 				}
-				ok = reads(u)
 			}
-			if ok {
-				want[id] = 1
+			if !takes {
+				halfOK[v] = false
 			}
 		}
-		return want[id] == 1
 	}
-	for i := range s.steps {
-		if !product(i) || !constWeight(&s.steps[i]) {
+
+	for j := range s.steps {
+		if !bf16Product(j) {
 			continue
 		}
-		if id := out0(i); id >= 0 {
-			if s.fuseAct[i] != 0 {
-				// the value that flows on is the activation node's output
-				s.halfOut[i] = wants(out0(users[id][0].step))
-			} else {
-				s.halfOut[i] = wants(id)
-			}
+		v := firstOut(j)
+		if v >= 0 && s.fuseAct[j] != 0 {
+			v = firstOut(lastStep[v]) // the value that flows on is the activation node's output
 		}
+		s.halfOut[j] = v >= 0 && halfOK[v]
 	}
 }
