@@ -230,11 +230,22 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* args);
  * INGOT_EINVAL and a message naming the size. No counterpart in the
  * reference: it is for callers that cannot allocate (HIP graph capture, tight
  * serving loops, harnesses that forbid it). The array is shared by every call
- * on that GPU, from any session or stream, and keeps the last call's contents
- * (each call writes every scratch byte it reads): calls that overlap on one GPU
- * race, so the caller serialises them. */
+ * on that GPU, from any session, and keeps the last call's contents (each call
+ * writes every scratch byte it reads). The library orders the calls: a call
+ * from one session makes its stream wait for the last no-alloc call another
+ * session made on that GPU, so they run in the order the host issued them.
+ * Two exceptions race on the array and are the caller's to order: calls made
+ * at the same moment from several host threads get some order, not theirs;
+ * and a stream under graph capture gets no such wait (the captured graph's
+ * replays must be ordered against other users of the array by the caller). */
 #define INGOT_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int ingot_rocm_gemm_noalloc(ingot_rocm_session* s, const ingot_rocm_gemm_args* args);
+
+/* Bytes of device memory the session's growable workspace holds now (0 until
+ * a call needs scratch: packed activations, GEMV x planes, int8 A, im2col).
+ * No counterpart in the reference: a diagnostic, e.g. to show that
+ * ingot_rocm_gemm_noalloc leaves the workspace unused. */
+int ingot_rocm_session_workspace(const ingot_rocm_session* s, size_t* bytes);
 
 /* Batched GEMM whose B is an activation: each batch item i multiplies its A
  * (stride_a) by its own B at d_b + i·stride_b elements (stride_b 0: one B for

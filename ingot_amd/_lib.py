@@ -65,6 +65,7 @@ SIGNATURES = {
     "ingot_rocm_last_error": (C.c_char_p, []),
     "ingot_rocm_version": (C.c_char_p, []),
     "ingot_rocm_sync": (C.c_int, [C.c_void_p]),
+    "ingot_rocm_session_workspace": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t)]),
     "ingot_rocm_stream": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
     "ingot_rocm_device_alloc": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p)]),
     "ingot_rocm_device_free": (C.c_int, [C.c_void_p, C.c_void_p]),

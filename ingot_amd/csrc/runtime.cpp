@@ -24,13 +24,27 @@ using namespace ingot;
 // quantised x) that ingot_rocm_gemm keeps in the session's growable
 // workspace. Each device holds its own copy for the life of the process. In
 // host code `scratch` only names the symbol: its device address comes from
-// hipGetSymbolAddress, once per device (g_scratch_addr), and only that
+// hipGetSymbolAddress, once per device (NoAllocDevice::addr), and only that
 // address is handed to kernels.
 constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
 static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 constexpr int kMaxDevices = 64;
+
+// Per device: the scratch array's address, and the ordering of the no-alloc
+// calls that share it. Sessions run on their own streams and calls return
+// before their kernels finish, so each call records `done` on its stream and
+// a call from another session first makes its stream wait for it: the
+// device's no-alloc calls run one after another in the order the host made
+// them, whichever sessions they come from. Set up when a session first opens
+// on the device (nothing is created in the call itself).
+struct NoAllocDevice {
+    void* addr = nullptr;
+    hipEvent_t done = nullptr;
+    const ingot_rocm_session* last = nullptr;  // session of the last recorded call
+    std::mutex mu;                             // orders the calls on the host
+};
 static std::mutex g_scratch_mu;
-static void* g_scratch_addr[kMaxDevices];
+static NoAllocDevice g_noalloc[kMaxDevices];
 
 namespace {
 
@@ -217,20 +231,24 @@ int ingot_rocm_open(int device, ingot_rocm_session** out) {
         return fail(INGOT_EDEVICE, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
     if (device >= kMaxDevices) return fail(INGOT_EINVAL, "device %d: at most %d devices", device, kMaxDevices);
     {
-        // with `device` current: its copy of the no-alloc scratch array
+        // with `device` current: its copy of the no-alloc scratch array and
+        // the event that orders the calls using it
         std::lock_guard<std::mutex> g(g_scratch_mu);
-        if (!g_scratch_addr[device]) {
+        NoAllocDevice& d = g_noalloc[device];
+        if (!d.addr) {
             void* p = nullptr;
             e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
             if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
             if (!p) return fail(INGOT_EDEVICE, "hipGetSymbolAddress(scratch) returned no address");
-            g_scratch_addr[device] = p;
+            e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
+            if (e != hipSuccess) return hip_fail(e, "no-alloc event");
+            d.addr = p;
         }
     }
     auto* s = new ingot_rocm_session();
     s->device = device;
     s->num_cus = prop.multiProcessorCount;
-    s->scratch = g_scratch_addr[device];
+    s->scratch = g_noalloc[device].addr;
     auto env_int = [](const char* name, int dflt) {
         const char* v = getenv(name);
         return v && *v ? atoi(v) : dflt;
@@ -257,6 +275,12 @@ int ingot_rocm_close(ingot_rocm_session* s) {
     if (!s) return INGOT_OK;
     (void)hipSetDevice(s->device);
     if (s->stream) (void)hipStreamSynchronize(s->stream);
+    if (s->device >= 0 && s->device < kMaxDevices) {
+        // its recorded no-alloc call is complete (the stream is drained)
+        NoAllocDevice& d = g_noalloc[s->device];
+        std::lock_guard<std::mutex> g(d.mu);
+        if (d.last == s) d.last = nullptr;
+    }
     for (auto* w : s->weights) {
         if (w->data) (void)hipFree(w->data);
         if (w->colsum) (void)hipFree(w->colsum);
@@ -679,7 +703,31 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
 int ingot_rocm_gemm_noalloc(ingot_rocm_session* s, const ingot_rocm_gemm_args* a) {
     int rc = validate_gemm(s, a, a ? a->w : nullptr);
     if (rc) return rc;
-    return gemm_core(s, a, a->w, 0, true);
+    NoAllocDevice& d = g_noalloc[s->device];
+    std::lock_guard<std::mutex> g(d.mu);
+    // Under stream capture the graph's own order applies (an event recorded
+    // outside the capture cannot be waited on inside it).
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s->stream, &cap);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    const bool order = cap == hipStreamCaptureStatusNone;
+    if (order && d.last && d.last != s) {
+        e = hipStreamWaitEvent(s->stream, d.done, 0);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
+    }
+    rc = gemm_core(s, a, a->w, 0, true);
+    if (rc == INGOT_OK && order) {
+        e = hipEventRecord(d.done, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+        d.last = s;
+    }
+    return rc;
+}
+
+int ingot_rocm_session_workspace(const ingot_rocm_session* s, size_t* bytes) {
+    if (!s || !bytes) return fail(INGOT_EINVAL, "nil argument");
+    *bytes = s->ws_bytes;
+    return INGOT_OK;
 }
 
 int ingot_rocm_gemm_dynamic_b(ingot_rocm_session* s, const ingot_rocm_gemm_args* a, const void* d_b, int32_t b_dtype,

@@ -169,6 +169,12 @@ class Session:
     def sync(self) -> None:
         L.check(self.lib.ingot_rocm_sync(self.h))
 
+    def workspace_bytes(self) -> int:
+        """Device bytes the session's growable workspace holds now (ingot_rocm_session_workspace)."""
+        n = C.c_size_t()
+        L.check(self.lib.ingot_rocm_session_workspace(self.h, C.byref(n)))
+        return n.value
+
     def timer_start(self) -> None:
         L.check(self.lib.ingot_rocm_timer_start(self.h))
 
