@@ -147,12 +147,16 @@ __device__ __forceinline__ float apply_act(float x, int act, float a, float b) {
         case INGOT_ACT_RELU: return fmaxf(x, 0.f);
         case INGOT_ACT_GELU_ERF: return 0.5f * x * (1.f + erf_as(x * 0.70710678118654752f));
         case INGOT_ACT_GELU_TANH: {
-            // tanh(v) = 1 − 2/(e^{2v} + 1) with the hardware exponential and
-            // reciprocal: a few ulp of 1 absolute, which is all 1 + tanh needs,
-            // and ±1 (not NaN) where e^{2v} overflows or vanishes
+            // 1 + tanh(v) from u = e^(−2|v|) ∈ [0, 1]: 2/(1 + u) for v >= 0 and
+            // 2u/(1 + u) for v < 0. Nothing cancels in the negative tail (x below
+            // about −3, where 1 + tanh(v) is tiny), so the result stays accurate
+            // relative to its value, and nothing overflows. The reference rounds
+            // tanh(v) to float32 before adding 1, an absolute error of up to
+            // 2^−25·|x| in that tail, which this stays within.
             const float v = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-            const float t = 1.f - 2.f * __builtin_amdgcn_rcpf(__expf(2.f * v) + 1.f);
-            return 0.5f * x * (1.f + t);
+            const float u = __expf(-2.f * fabsf(v));
+            const float g = (v < 0.f ? 2.f * u : 2.f) * __builtin_amdgcn_rcpf(1.f + u);
+            return 0.5f * x * g;
         }
         // IEEE quotients: past x = −87.3 the clamped 1 + e^(−x) exceeds 2^126, and
         // the hardware reciprocal would flush 1/(1 + e^(−x)) to zero where the

@@ -296,9 +296,14 @@ def test_activation_nodes(sess, name, domain, attrs, code):
                                       (L.ACT_HARDSIGMOID, 0.2, 0.5), (L.ACT_CLIP, -1.5, 2.0), (L.ACT_LEAKYRELU, 0.1, 0)])
 def test_activation_special_values(sess, code, a, b):
     """Every activation of the epilogue set on NaN, ±Inf, ±0, huge and exp-saturating inputs, against the
-    oracle: NaN where it gives NaN (the clamps of expScalar, clip and hardsigmoid compare, as Go's min/max do,
-    so a NaN passes through: kernels/vek/scalar.go:11-13, kernels/vek/vek_generic.go:48-76), the same ±Inf,
-    and finite values within 2e-6 relative."""
+    oracle: NaN where it gives NaN, the same ±Inf, and finite values within 2e-6 relative.
+
+    NaN through the clamps (expScalar's, clip, hardsigmoid) is where the reference disagrees with itself across
+    platforms: its arm64 vector kernels (FMAX/FMIN, kernels/vek/vek_arm64.s) and its scalar tails (Go's min/max,
+    kernels/vek/scalar.go:11-13, kernels/vek/vek_generic.go:48-76) pass a NaN through, while its amd64 vector
+    bodies (VMAXPS/VMINPS, kernels/vek/genamd64/main.go:241-256) return the bound: clip(NaN) = lo and
+    hardsigmoid(NaN) = 0 there. This library follows arm64 and the scalar code (NaN out), and the oracle pins
+    that choice."""
     announce(f"activation special values act={code}")
     special = [np.nan, np.inf, -np.inf, 0.0, -0.0, 1e30, -1e30, 3.4e38, -3.4e38, 100.0, -100.0, 88.5, -88.5,
                87.4, -87.4, 20.0, -20.0, 1e-30, -1e-30, 0.5, -0.5, 3.0, -3.0]
@@ -314,6 +319,42 @@ def test_activation_special_values(sess, code, a, b):
     fin = np.isfinite(want)
     err = np.abs(got[fin] - want[fin]) / np.maximum(1.0, np.abs(want[fin]))
     assert err.max() <= 2e-6, f"act {code}: relative error {err.max():.3e} at {x[0][fin][np.argmax(err)]}"
+
+
+def test_gelu_tanh_negative_tail_relative(sess):
+    """GELU-tanh over a dense sweep of x in [-8, -2], where 1 + tanh(v) is tiny (ops/elementwise.go:411-414): the
+    activation kernel and the f32 GEMM epilogue (both apply_act; the product is x·1 exactly) hold a bound relative
+    to the float64 value, 2e-5·|want| (the float32 evaluation of v moves the result by a few 1e-6 relative
+    there). The reference rounds tanh(v) to float32 before adding 1, so its own values in this range are off by up
+    to 2^-25·|x| absolute; the bound is far inside that too."""
+    announce("gelu-tanh negative tail")
+    x = np.linspace(-8.0, -2.0, 20001).astype(np.float32)
+    # in float64 through 1 + tanh(v) = 2 / (1 + e^(-2v)): the formula's own 1 + tanh(v) cancels in float64 as
+    # well once v < -13 (x below about -5.4), where it returns 0 or one ulp of 1
+    xd = x.astype(np.float64)
+    want = xd / (1.0 + np.exp(-2.0 * 0.7978845608028654 * (xd + 0.044715 * xd ** 3)))
+    mid = np.abs(xd) < 4.5  # where the float64 formula is still accurate, the identity must agree with it
+    direct = np.array([oracle.act(float(v), L.ACT_GELU_TANH) for v in xd[mid]])
+    assert np.allclose(want[mid], direct, rtol=1e-8, atol=0)
+    tol = 2e-5 * np.abs(want)
+    y = sess.empty(L.DT_F32, (1, x.size))
+    sess.activation(dev(sess, x.reshape(1, -1)), y, 1, x.size, L.ACT_GELU_TANH)
+    got = y.numpy()[0].astype(np.float64)
+    bad = np.abs(got - want) > tol
+    assert not bad.any(), f"activation: {bad.sum()} values off, worst at x={x[np.argmax(np.abs(got - want) / tol)]}"
+    # the fused epilogue: A[i] = (x_i, 0, ..., 0), every weight row = e_0 (f32 weights: the product is exact)
+    k, n = 64, 16
+    a = np.zeros((x.size, k), np.float32)
+    a[:, 0] = x
+    w = np.zeros((n, k), np.float32)
+    w[:, 0] = 1.0
+    wt = sess.upload_weight(w, trans=True, pack_dtype=L.DT_F32)
+    yg = sess.empty(L.DT_F32, (x.size, n))
+    sess.gemm(dev(sess, a), wt, yg, x.size, act=L.ACT_GELU_TANH)
+    got = yg.numpy().astype(np.float64)
+    bad = np.abs(got - want[:, None]) > tol[:, None]
+    assert not bad.any(), f"GEMM epilogue: {bad.sum()} values off"
+    wt.free()
 
 
 def test_refilled_weight_buffer_is_repacked(sess):
