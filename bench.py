@@ -284,6 +284,64 @@ class Dit:
             wt.free()
             del ta, tw
 
+    def sequence_probe(self, reps: int = 10):
+        """Per-launch GPU time of each DiT GEMM kernel (bf16 activations, as `roofline` launches them) in four
+        orders: the bench's sequence (QKV, MLP-up, MLP-down, repeated), one GEMM repeated alone (its operands stay
+        in the Infinity Cache), and each GEMM after filling 1 GiB (a write pass: the cache full of dirty lines)
+        or after reading 1 GiB (a 1 GiB f32 → bf16 cast: mostly clean lines). HIP events on the session stream
+        around each launch, no synchronisation between launches; medians over `reps`. INGOT_GEMM_CFG selects a
+        tile for all three GEMMs. The sequence runs for about a second first, and is measured again at the end.
+        One JSON line."""
+        import ctypes as C
+
+        import torch
+
+        L, s = self.L, self.sess
+        a16 = {}
+        for k, t in self.a.items():
+            a16[k] = s.empty(L.DT_BF16, (self.M, k))
+            s.cast_bf16(t, a16[k])
+        calls = {tag: s.prepare_gemm(a16[k], w, y, self.M, act=act, a_dtype=L.DT_BF16)
+                 for (k, n, tag), w, y, act in zip(self.shapes, self.w, self.y, self.acts)}
+        fill = s.empty(L.DT_U8, (1 << 30,))
+        src, dst = s.empty(L.DT_F32, (1 << 28,)), s.empty(L.DT_BF16, (1 << 28,))
+        st = C.c_void_p()
+        L.check(s.lib.ingot_rocm_stream(s.h, C.byref(st)))
+        ext = torch.cuda.ExternalStream(st.value)
+
+        def timed(order, n):
+            evs = []
+            for _ in range(n):
+                for item in order:
+                    if isinstance(item, str):
+                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        e0.record(ext)
+                        calls[item]()
+                        e1.record(ext)
+                        evs.append((item, e0, e1))
+                    else:
+                        item()
+            s.sync()
+            torch.cuda.synchronize()
+            out = {}
+            for tag, e0, e1 in evs:
+                out.setdefault(tag, []).append(e0.elapsed_time(e1) * 1e3)
+            return {t: round(float(np.median(v)), 1) for t, v in out.items()}
+
+        tags = [t for _, _, t in self.shapes]
+        wflush, rflush = (lambda: s.memset(fill, 0)), (lambda: s.cast_bf16(src, dst))
+        t_end = time.perf_counter() + 1.0  # about a second of the sequence first: the clock leaves its idle state
+        while time.perf_counter() < t_end:
+            timed(tags, 4)
+        res = {"gemm_cfg": os.environ.get("INGOT_GEMM_CFG", "default"), "sequence": timed(tags, reps)}
+        res["alone"] = {t: timed([t], reps)[t] for t in tags}
+        res["after_1GiB_fill"] = timed([x for t in tags for x in (wflush, t)], reps // 2)
+        res["after_1GiB_read"] = timed([x for t in tags for x in (rflush, t)], reps // 2)
+        res["sequence_again"] = timed(tags, reps)
+        print(json.dumps(res), flush=True)
+        for t in list(a16.values()) + [fill, src, dst]:
+            t.free()
+
     def probe(self):
         """One plain copy of PROBE_COPY_BYTES (counter calibration), then one launch of each GEMM."""
         L, s = self.L, self.sess
@@ -502,21 +560,25 @@ class Decode:
     def compare_stream_read(self, reps: int = 20):
         """The M = 1 GEMV of each decode shape against reading the same weight bytes with vendor code: a
         torch.sum over a bf16 tensor of the weight's shape (torch's reduction kernel, f32 accumulation), and a
-        device-to-device torch copy of the same bytes (which also writes them). Each side rotates over
-        `copies` distinct buffers (beyond the Infinity Cache together), timed with HIP events over `reps`
-        launches, four alternating rounds; the minimum of each is compared. One JSON line per shape."""
+        device-to-device torch copy of the same bytes (which also writes them). Each side rotates over as many
+        distinct buffers as exceed 320 MB together (beyond the 256 MB Infinity Cache, so HBM serves them), timed
+        with HIP events over `reps` passes, four alternating rounds; the minimum of each is compared. One JSON
+        line per shape."""
         import torch
 
         s = self.sess
         rng = np.random.default_rng(self.seed)
         for j, (k, n) in enumerate(self.shapes):
-            tw = [torch.from_numpy(normal32(rng, (n, k), 0.02)).to("cuda").to(torch.bfloat16)
-                  for _ in range(self.copies)]
+            copies = int(np.ceil(320e6 / (2.0 * n * k)))
+            wh = normal32(rng, (n, k), 0.02)
+            tw = [torch.from_numpy(wh).to("cuda").to(torch.bfloat16) for _ in range(copies)]
             dst = torch.empty_like(tw[0])
+            ws = [s.upload_weight(wh, trans=True, pack_dtype=self.L.DT_BF16) for _ in range(copies)]
+            calls = [s.prepare_gemm(self.x[k], w, self.y[j], 1) for w in ws]
 
             def ours():
-                for c in range(self.copies):
-                    self.calls[1][c][j]()
+                for call in calls:
+                    call()
 
             def torch_ms(fn):
                 fn()
@@ -539,16 +601,18 @@ class Decode:
 
             g, r, cp = [], [], []
             for _ in range(4):
-                g.append(event_ms(s, ours, reps) / self.copies * 1e3)
-                r.append(torch_ms(tsum) / self.copies * 1e3)
-                cp.append(torch_ms(copy) / self.copies * 1e3)
+                g.append(event_ms(s, ours, reps) / copies * 1e3)
+                r.append(torch_ms(tsum) / copies * 1e3)
+                cp.append(torch_ms(copy) / copies * 1e3)
             wb = 2.0 * n * k
-            print(json.dumps({"shape": f"{k}x{n}", "weight_MB": round(wb / 1e6, 2),
+            print(json.dumps({"shape": f"{k}x{n}", "weight_MB": round(wb / 1e6, 2), "copies": copies,
                               "gemv_m1_us": round(min(g), 2), "gemv_m1_GB_per_s": round(wb / min(g) / 1e3, 1),
                               "torch_sum_us": round(min(r), 2), "torch_sum_GB_per_s": round(wb / min(r) / 1e3, 1),
                               "d2d_copy_us": round(min(cp), 2), "d2d_copy_read_GB_per_s": round(wb / min(cp) / 1e3, 1)}),
                   flush=True)
             del tw, dst
+            for w in ws:
+                w.free()
 
     def bytes_step(self, M):
         return self.wbytes + sum(4.0 * M * (k + n) for k, n in self.shapes)
@@ -590,18 +654,27 @@ class Decode:
                 # a decode-step rate (weight + activation bytes over the step), not one kernel's HBM roofline
                 leg["step_bytes_frac_of_hbm"] = round(gbs / PEAK["hbm"], 4)
             out[f"m{M}"] = leg
-        # per-shape kernel time at M=1 (events over rotated launches), after a
-        # warm-up pass over every shape so the first one timed is not the one
-        # that follows the M=16 leg
+        # per-shape time at M = 1: back-to-back launches of one shape (HIP events) rotating over as many copies
+        # of its weight as exceed 320 MB together, so HBM serves them and not the 256 MB Infinity Cache
+        # (three copies of one shape would fit in it)
         per = {}
-        time_steps(self.sess, lambda: self.step(1), 20, 0)
+        rng = np.random.default_rng(self.seed + 7)
         for j, (k, n) in enumerate(self.shapes):
-            def launches(j=j):
-                for c in range(self.copies):
-                    self.calls[1][c][j]()
-            ms = event_ms(self.sess, launches, 50) / self.copies
-            b = 2.0 * n * k + 4.0 * (k + n)
-            per[f"{k}x{n}"] = {"us": round(ms * 1e3, 2), "GB_per_s": round(b / (ms * 1e-3) / 1e9, 1)}
+            wb = 2.0 * n * k
+            wh = normal32(rng, (n, k), 0.02)
+            ws = [self.sess.upload_weight(wh, trans=True, pack_dtype=self.L.DT_BF16)
+                  for _ in range(int(np.ceil(320e6 / wb)))]
+            calls = [self.sess.prepare_gemm(self.x[k], w, self.y[j], 1) for w in ws]
+
+            def launches():
+                for call in calls:
+                    call()
+            ms = event_ms(self.sess, launches, 10) / len(calls)
+            b = wb + 4.0 * (k + n)
+            per[f"{k}x{n}"] = {"us": round(ms * 1e3, 2), "GB_per_s": round(b / (ms * 1e-3) / 1e9, 1),
+                               "copies": len(calls)}
+            for w in ws:
+                w.free()
         out["m1_per_shape"] = per
         # the same step on grouped-int8 weights (ingot_weight_quant="int8"): bytes = int8 weights + f32 scales
         L = self.L
@@ -708,19 +781,20 @@ def main() -> int:
     ap.add_argument("--cpu-seconds-extra", type=float, default=3.0,
                     help="CPU-baseline time budget of each other workload")
     ap.add_argument("--probe", nargs="?", const="dit",
-                    choices=["dit", "decode", "bert", "int8", "hipblaslt", "streamread"],
+                    choices=["dit", "decode", "bert", "int8", "hipblaslt", "streamread", "sequence"],
                     help="counter probe for rocprofv3 --pmc: one calibration copy, then one launch of each DiT GEMM "
                          "(dit, the default) or one decode GEMV step at M = 1, 4, 16 (decode); bert: one launch of "
                          "each BERT f32 projection; int8: one calibration copy, then one MatMulInteger + dequant call; "
                          "hipblaslt: the DiT GEMM kernel against hipBLASLt on the same operands (one JSON line each); "
                          "streamread: the M = 1 decode GEMVs against a vendor read (torch.sum) and a device copy of the "
-                         "same weight bytes (one JSON line each)")
+                         "same weight bytes (one JSON line each); sequence: per-launch times of the DiT GEMM kernels "
+                         "in the bench's order, alone, and after a 1 GiB write or read pass (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         log("bench.py: this build measures one GPU (the path has no multi-GPU component); run with --gpus 1")
         return 2
 
-    if args.probe in ("hipblaslt", "streamread"):
+    if args.probe in ("hipblaslt", "streamread", "sequence"):
         # torch's HIP runtime is loaded and initialised before the library's (started the other way round,
         # torch finds no GPU)
         import torch
@@ -732,6 +806,10 @@ def main() -> int:
     sess = Session(0)
     if args.probe == "hipblaslt":
         Dit(sess, L).compare_hipblaslt()
+        sess.close()
+        return 0
+    if args.probe == "sequence":
+        Dit(sess, L).sequence_probe()
         sess.close()
         return 0
     if args.probe == "streamread":
