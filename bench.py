@@ -283,6 +283,70 @@ class Dit:
                 t.free()
             wt.free()
             del ta, tw
+        self.compare_hipblaslt_sequence()
+
+    def compare_hipblaslt_sequence(self, reps: int = 10, rounds: int = 4):
+        """The same comparison in the bench's order (QKV, MLP-up, MLP-down, repeated; no epilogue on either
+        side), after about a second of both sequences: per-launch HIP events, medians per round, the two sides
+        alternating round by round. One JSON line."""
+        import ctypes as C
+
+        import torch
+
+        L, s = self.L, self.sess
+        rng = np.random.default_rng(self.seed)
+        ours, theirs = {}, {}
+        keep = []
+        for k, n, tag in self.shapes:
+            a = rng.normal(0, 1, (self.M, k)).astype(np.float32)
+            w = normal32(rng, (n, k), 0.02)
+            da = s.to_device(a)
+            a16 = s.empty(L.DT_BF16, (self.M, k))
+            s.cast_bf16(da, a16)
+            wt = s.upload_weight(w, trans=True, pack_dtype=L.DT_BF16)
+            y = s.empty(L.DT_F32, (self.M, n))
+            ours[tag] = s.prepare_gemm(a16, wt, y, self.M, a_dtype=L.DT_BF16)
+            ta = torch.from_numpy(a).to("cuda").to(torch.bfloat16)
+            tw = torch.from_numpy(w).to("cuda").to(torch.bfloat16)
+            theirs[tag] = (lambda ta=ta, tw=tw: torch.mm(ta, tw.t(), out_dtype=torch.float32))
+            keep += [da, a16, y, wt, ta, tw]
+        st = C.c_void_p()
+        L.check(s.lib.ingot_rocm_stream(s.h, C.byref(st)))
+        ext = torch.cuda.ExternalStream(st.value)
+        cur = torch.cuda.current_stream()
+        tags = [t for _, _, t in self.shapes]
+
+        def timed(fns, stream, n):
+            evs = []
+            for _ in range(n):
+                for t in tags:
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    fns[t]()
+                    e1.record(stream)
+                    evs.append((t, e0, e1))
+            s.sync()
+            torch.cuda.synchronize()
+            out = {}
+            for t, e0, e1 in evs:
+                out.setdefault(t, []).append(e0.elapsed_time(e1) * 1e3)
+            return {t: round(float(np.median(v)), 1) for t, v in out.items()}
+
+        t_end = time.perf_counter() + 1.0
+        while time.perf_counter() < t_end:
+            timed(ours, ext, 2)
+            timed(theirs, cur, 2)
+        r_ours, r_theirs = [], []
+        for _ in range(rounds):
+            r_ours.append(timed(ours, ext, reps))
+            r_theirs.append(timed(theirs, cur, reps))
+        avg = lambda r: round(sum(r.values()) / len(r), 1)
+        print(json.dumps({"sequence": "qkv, mlp_up (no epilogue), mlp_down, repeated", "ours_us": r_ours,
+                          "hipblaslt_us": r_theirs, "ours_avg_per_round": [avg(r) for r in r_ours],
+                          "hipblaslt_avg_per_round": [avg(r) for r in r_theirs]}), flush=True)
+        for t in keep:
+            if hasattr(t, "free"):
+                t.free()
 
     def sequence_probe(self, reps: int = 10):
         """Per-launch GPU time of each DiT GEMM kernel (bf16 activations, as `roofline` launches them) in four
@@ -700,20 +764,28 @@ class Decode:
         return out
 
     def cpu_baseline(self, info, seconds: float):
-        """The M = 1 decode step on the host: the four bf16-weight GEMVs with a widening dot (GemvBF16)."""
+        """The M = 1 decode step on the host: the four bf16-weight GEMVs with a widening dot (GemvBF16),
+        successive steps rotating over four copies of the weights (412 MB), so that the host's caches cannot
+        hold the weights of the step they serve, as the GPU side rotates its copies beyond the Infinity Cache."""
         import oracle
 
         rng = np.random.default_rng(self.seed)
         xs = {k: rng.normal(0, 1, (1, k)).astype(np.float32) for k in (2048, 5632)}
         ws = [oracle.f32_to_bf16(normal32(rng, (n, k), 0.02)) for k, n in self.shapes]
+        copies = 4
+        sets = [ws] + [[w.copy() for w in ws] for _ in range(copies - 1)]
+        turn = [0]
 
         def once():
-            for (k, n), w in zip(self.shapes, ws):
+            cur = sets[turn[0] % copies]
+            turn[0] += 1
+            for (k, n), w in zip(self.shapes, cur):
                 oracle.base_gemv_bf16(xs[k], w, threads=info["threads"])
 
         t, reps = cpu_time(once, seconds)
         return cpu_entry(round(self.bytes_step(1) / t / 1e9, 2), "GB/s", info,
-                         f"the M = 1 decode step (4 GEMVs, 103 MB of bf16 weights); median of {reps} steps",
+                         f"the M = 1 decode step (4 GEMVs, 103 MB of bf16 weights), steps rotating over {copies} "
+                         f"weight copies ({copies * self.wbytes / 1e6:.0f} MB); median of {reps} steps",
                          us_per_step=round(t * 1e6, 1))
 
 
