@@ -749,6 +749,43 @@ def test_deep_prefetch_tile_m_invariant(env_session):
             assert np.array_equal(rows[("plain", M)], rows[("deep", m)][:M]), f"deep tile rows differ at M={M} {kw}"
 
 
+@pytest.mark.parametrize("k", [1, 33, 64, 65, 128, 200])
+def test_deep_prefetch_tile_short_and_batched(env_session, k):
+    """The register-staged 256×192 tile forced (INGOT_GEMM_CFG=9) where its pipeline runs out early: K of one
+    k-tile or less (the loads of k-tiles 1..3 are past the end from the start), K of one and two k-tiles exactly
+    and ragged; bf16 A and the hi/lo split (two virtual k-tiles per k-tile), a bias and GELU in the epilogue,
+    ragged M and N; and a batched per-item B (ingot_rocm_gemm_dynamic_b) whose items the grid's y index selects."""
+    announce(f"deep-prefetch tile short k={k}")
+    sess = env_session(INGOT_GEMM_CFG=9)
+    rng = np.random.default_rng(1000 + k)
+    m, n = 300, 250
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    bt = bf16_weights(rng, (n, k), 0.05, "normal")
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    w = sess.upload_weight(bt, trans=True, pack_dtype=L.DT_BF16, src_dtype=L.DT_BF16)
+    wide = oracle.bf16_to_f32(bt)
+    for kind, kw in (("bf16", {"math": L.MATH_BF16}), ("hilo", {})):
+        ain = oracle.bf16_to_f32(oracle.f32_to_bf16(a)) if kind == "bf16" else a
+        y = sess.empty(L.DT_F32, (m, n))
+        sess.gemm(sess.to_device(a), w, y, m, beta=1.0, c=sess.to_device(bias), c_mode=L.C_ROW, act=L.ACT_GELU_ERF,
+                  **kw)
+        want = oracle.gemm(np.ascontiguousarray(ain), bt, trans_b=True, b_dtype=oracle.BF16, c=bias, c_mode=L.C_ROW,
+                           beta=1.0, act_code=L.ACT_GELU_ERF)
+        assert_close(y.numpy(), want, nstar_tol(k, a, wide), f"deep tile {kind} k={k}")
+    w.free()
+    bsz = 3
+    ab = rng.normal(0, 1, (bsz, m, k)).astype(np.float32)
+    bb = bf16_weights(rng, (bsz, n, k), 0.05, "normal")
+    y = sess.empty(L.DT_F32, (bsz, m, n))
+    sess.gemm_dynamic_b(sess.to_device(ab), sess.to_device(bb, L.DT_BF16), y, m, n, k, True, k, n * k, batch=bsz,
+                        stride_a=m * k, stride_y=m * n, math=L.MATH_BF16)
+    got = y.numpy()
+    for i in range(bsz):
+        ain = oracle.bf16_to_f32(oracle.f32_to_bf16(ab[i]))
+        want = oracle.gemm(np.ascontiguousarray(ain), bb[i], trans_b=True, b_dtype=oracle.BF16)
+        assert_close(got[i], want, nstar_tol(k, ab, oracle.bf16_to_f32(bb[i])), f"deep tile batched item {i}")
+
+
 @pytest.mark.parametrize("n,k", [(2048, 2048), (6144, 2048), (2048, 5632), (1000, 1300)])
 def test_gemv_rows_m_invariant(sess, n, k):
     """The decode GEMV among itself: the M = 1 row kernel and the LDS-DMA kernel (M = 2..4 with K % 4 == 0 and
