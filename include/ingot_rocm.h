@@ -233,11 +233,11 @@ int ingot_rocm_gemm(ingot_rocm_session* s, const ingot_rocm_gemm_args* args);
  * on that GPU, from any session, and keeps the last call's contents (each call
  * writes every scratch byte it reads). The library orders the calls: a call
  * from one session makes its stream wait for the last no-alloc call another
- * session made on that GPU, so they run in the order the host issued them.
- * Two exceptions race on the array and are the caller's to order: calls made
- * at the same moment from several host threads get some order, not theirs;
- * and a stream under graph capture gets no such wait (the captured graph's
- * replays must be ordered against other users of the array by the caller). */
+ * session made on that GPU, so they run in the order the host issued them
+ * (calls made at the same moment from several host threads still run one
+ * after another, in an order the library picks). A stream under graph capture
+ * gets no such wait: the captured graph's replays race on the array with its
+ * other users unless the caller orders them. */
 #define INGOT_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int ingot_rocm_gemm_noalloc(ingot_rocm_session* s, const ingot_rocm_gemm_args* args);
 

@@ -716,9 +716,11 @@ int ingot_rocm_gemm_noalloc(ingot_rocm_session* s, const ingot_rocm_gemm_args* a
         if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent");
     }
     rc = gemm_core(s, a, a->w, 0, true);
-    if (rc == INGOT_OK && order) {
+    if (order) {
+        // recorded after a failed call too: a kernel it enqueued before failing
+        // may still use the array
         e = hipEventRecord(d.done, s->stream);
-        if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+        if (e != hipSuccess) return rc ? rc : hip_fail(e, "hipEventRecord");
         d.last = s;
     }
     return rc;
