@@ -786,6 +786,63 @@ def test_deep_prefetch_tile_short_and_batched(env_session, k):
         assert_close(got[i], want, nstar_tol(k, ab, oracle.bf16_to_f32(bb[i])), f"deep tile batched item {i}")
 
 
+@pytest.mark.parametrize("seed", range(32))
+def test_random_products_against_oracle(sess, seed):
+    """Seeded random products through ingot_rocm_gemm against the float64 oracle: shapes from 1 to a few hundred
+    rows (so the decode GEMV, the small-tile and the large-tile GEMMs all take part), f32 or bf16 weights in either
+    source layout, the default and the bf16 math, transposed A (f32 weights), every C mode with random α and β,
+    every activation, the post scale and shift, a Y pitch wider than N and bf16 Y. Bound: the north-star max-abs
+    bound scaled by |α|, the activation's slope (at most 2) and the post scale, plus bf16 Y's rounding."""
+    rng = np.random.default_rng(9000 + seed)
+
+    def dim(lo, hi):
+        return int(np.exp(rng.uniform(np.log(lo), np.log(hi + 1))))
+
+    m, n, k = dim(1, 600), dim(16, 1500), dim(24, 2100)
+    wdt = ["f32", "bf16"][rng.integers(2)]
+    math_mode = L.MATH_BF16 if wdt == "bf16" and rng.integers(3) == 0 else L.MATH_AUTO
+    trans_a = wdt == "f32" and bool(rng.integers(2))
+    src_kn = bool(rng.integers(2))
+    c_mode = int(rng.integers(5))
+    act = int(rng.integers(10))
+    aa, ab = {L.ACT_HARDSIGMOID: (0.2, 0.5), L.ACT_CLIP: (-0.4, 0.6), L.ACT_LEAKYRELU: (0.03, 0.0)}.get(act, (0.0, 0.0))
+    alpha = float(rng.choice([1.0, 0.5, -1.25]))
+    beta = float(rng.choice([0.0, 1.0, -0.75])) if c_mode else 0.0
+    post = bool(rng.integers(2))
+    ps, pt = (1.5, -0.25) if post else (1.0, 0.0)
+    ybf16 = bool(rng.integers(4) == 0)
+    ldy = n + int(rng.choice([0, 0, 4, 5]))
+    announce(f"random product seed={seed} m={m} n={n} k={k} w={wdt} math={math_mode} transA={trans_a} "
+             f"c_mode={c_mode} act={act} ybf16={ybf16} ldy={ldy}")
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    bt = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    if wdt == "bf16":
+        bt = oracle.bf16_to_f32(oracle.f32_to_bf16(bt))
+    src = np.ascontiguousarray(bt.T) if src_kn else bt
+    w = sess.upload_weight(src, trans=not src_kn, pack_dtype=L.DT_F32 if wdt == "f32" else L.DT_BF16)
+    c = {L.C_FULL: rng.normal(0, 1, (m, n)), L.C_ROW: rng.normal(0, 1, n), L.C_COL: rng.normal(0, 1, m),
+         L.C_SCALAR: rng.normal(0, 1, 1)}.get(c_mode)
+    c = None if c is None else c.astype(np.float32)
+    da = sess.to_device(np.ascontiguousarray(a.T) if trans_a else a)
+    y = sess.empty(L.DT_BF16 if ybf16 else L.DT_F32, (m, ldy))
+    kw = dict(trans_a=trans_a, alpha=alpha, beta=beta, act=act, act_alpha=aa, act_beta=ab, post=post,
+              post_scale=ps, post_shift=pt, ldy=ldy, math=math_mode)
+    if c is not None:
+        kw.update(c=sess.to_device(c), c_mode=c_mode)
+    sess.gemm(da, w, y, m, **kw)
+    got = y.numpy()[:, :n]
+    got = oracle.bf16_to_f32(got) if ybf16 else got
+    ain = oracle.bf16_to_f32(oracle.f32_to_bf16(a)) if math_mode == L.MATH_BF16 else a
+    want = oracle.gemm(ain, bt, trans_b=True, alpha=alpha, beta=beta, c=c, c_mode=c_mode if c is not None else 0,
+                       ldc=n if c_mode == L.C_FULL else 0, act_code=act, act_alpha=aa, act_beta=ab, post=post,
+                       post_scale=ps, post_shift=pt)
+    tol = 2.0 * abs(alpha) * ps * nstar_tol(k, a, bt) + 1e-5
+    if ybf16:
+        tol += float(np.max(np.abs(want))) * 2.0 ** -8
+    assert_close(got, want, tol, f"random product seed {seed}")
+    w.free()
+
+
 @pytest.mark.parametrize("n,k", [(2048, 2048), (6144, 2048), (2048, 5632), (1000, 1300)])
 def test_gemv_rows_m_invariant(sess, n, k):
     """The decode GEMV among itself: the M = 1 row kernel and the LDS-DMA kernel (M = 2..4 with K % 4 == 0 and
