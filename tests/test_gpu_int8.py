@@ -132,3 +132,42 @@ def test_qlinear_matmul_exact(sess, m, k, n, a_dt, za, ydt, zy):
     got = y.numpy()
     assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {got.size} differ"
     w.free()
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_matmul_integer_exact(sess, seed):
+    """Seeded random MatMulInteger calls, bit-exact against the oracle's closed form: shapes from 1 up to
+    configs[2] size, u8 or s8 activations with any zero point of their type, the full s8 weight range (−128 too)
+    in either source layout, an activation pitch wider than K, and the int32 output, the fused per-column or
+    per-tensor dequantisation with a zero point, or both."""
+    rng = np.random.default_rng(7000 + seed)
+
+    def dim(lo, hi):
+        return int(np.exp(rng.uniform(np.log(lo), np.log(hi + 1))))
+
+    m, k, n = dim(1, 800), dim(1, 1600), dim(1, 2500)
+    a_dt = [np.uint8, np.int8][rng.integers(2)]
+    info = np.iinfo(a_dt)
+    za = int(rng.integers(info.min, info.max, endpoint=True))
+    lda = k + int(rng.choice([0, 0, 3, 16]))
+    kn = bool(rng.integers(2))
+    outs = ["i32", "f32", "both"][rng.integers(3)]
+    per_col = bool(rng.integers(2))
+    dq_zp = int(rng.integers(-40, 41))
+    announce(f"int8 random seed={seed} m={m} k={k} n={n} a={np.dtype(a_dt).name} za={za} lda={lda} "
+             f"kn={kn} outs={outs} per_col={per_col}")
+    a = rng.integers(info.min, info.max, (m, lda), endpoint=True).astype(a_dt)
+    b = rng.integers(-128, 127, (k, n), endpoint=True).astype(np.int8)
+    w = sess.upload_weight(b if kn else np.ascontiguousarray(b.T), trans=not kn, pack_dtype=L.DT_I8)
+    scale = rng.uniform(0.001, 0.01, n if per_col else 1).astype(np.float32)
+    yi = sess.empty(L.DT_I32, (m, n)) if outs in ("i32", "both") else None
+    yf = sess.empty(L.DT_F32, (m, n)) if outs in ("f32", "both") else None
+    sess.matmul_integer(sess.to_device(a, L.DT_U8 if a_dt == np.uint8 else L.DT_I8), w, m, za, y_i32=yi,
+                        scale=sess.to_device(scale) if yf is not None else None, dq_zp=dq_zp, y_f32=yf, lda=lda)
+    want = oracle.matmul_integer(np.ascontiguousarray(a[:, :k]), b, za)
+    if yi is not None:
+        assert np.array_equal(yi.numpy(), want), f"int32 seed {seed}"
+    if yf is not None:
+        wf = oracle.dequantize_linear(want, scale, inner=1, zp=np.array([dq_zp], np.int32))
+        assert np.array_equal(yf.numpy(), wf), f"dequant seed {seed}"
+    w.free()
