@@ -16,8 +16,9 @@ int8 MatMulInteger + DequantizeLinear and decode GEMV M=1/4/16
 Cache, serves them).
 
 roofline: the dominant kernel's algorithmic FLOPs (or bytes) per launch over
-its average launch duration, timed with HIP events on the session stream
-(the stream the kernels run on). roofline.traffic is the kernel's HBM bytes
+its average launch duration in steady state (after ROOFLINE_WARM untimed
+passes), timed with HIP events on the session stream (the stream the kernels
+run on). roofline.traffic is the kernel's HBM bytes
 per launch as counted by rocprofv3 (FETCH_SIZE + WRITE_SIZE, each scaled by
 what the counter reads for a plain copy of known size) over `bench.py
 --probe`; the summary, with its commands, is profiles/dit_gemm_traffic.md,
@@ -42,6 +43,10 @@ METRIC = "GEMM TFLOPS (bf16/fp32), int8 TOPS, GEMV HBM GB/s; % of MI355X rooflin
 PEAK = {"bf16": 2516.6, "f32": 157.3, "i8": 5033.2, "hbm": 8000.0}  # TFLOP/s, TOP/s, GB/s
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "dit_gemm_traffic.md")
 PROBE_COPY_BYTES = 256 << 20
+# Untimed passes of the three DiT GEMMs before `roofline` times ten: about 30 ms of sustained load,
+# over which the MI355X clock settles (it is still rising during the headline's warm-up when that
+# is the driver's 5 steps), so `roofline` describes the kernel in steady state, as the profiles do.
+ROOFLINE_WARM = 40
 
 
 def measured_traffic():
@@ -123,9 +128,10 @@ def cpu_entry(value, unit, info, kind_sample, **extra):
     return out
 
 
-def event_ms(sess, fn, reps: int) -> float:
-    """Average GPU time of fn() (HIP events on the session stream)."""
-    fn()
+def event_ms(sess, fn, reps: int, warm: int = 1) -> float:
+    """Average GPU time of fn() (HIP events on the session stream) after `warm` untimed calls."""
+    for _ in range(warm):
+        fn()
     sess.sync()
     sess.timer_start()
     for _ in range(reps):
@@ -192,7 +198,7 @@ class Dit:
             for call in calls:
                 call()
 
-        ms = event_ms(s, launches, 10) / len(self.shapes)
+        ms = event_ms(s, launches, 10, warm=ROOFLINE_WARM) / len(self.shapes)
         flops = self.flops / len(self.shapes)
         for t in a16.values():
             t.free()
@@ -222,7 +228,7 @@ class Dit:
             for call in calls:
                 call()
 
-        ms = event_ms(s, launches, 10) / len(self.shapes)
+        ms = event_ms(s, launches, 10, warm=ROOFLINE_WARM) / len(self.shapes)
         for t in a16.values():
             t.free()
         for w in ws:
